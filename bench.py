@@ -1,0 +1,211 @@
+"""Benchmark of the identical-mode FP32 GEMM/GEMV on one MI355X.
+
+Headline (the JSON line's `value`): the decoder-LM prefill projection, X[2048x4096] . W[4096x4096]
++ bias[4096] under mojolearn.identical.gemm.fp32.v1 (nn.Linear bias fused into the store),
+inputs resident in HBM, one product per step, in TFLOP/s (2mnk per step; the bias adds are not
+counted).  Beside it: the kernel's roofline fraction (FP32 matrix peak 157.3 TFLOP/s), the
+other workloads (--all: 512^3, decode GEMV with an int8 weight at M = 1/4/16 in GB/s, the bf16
+SwiGLU up projection, the adversarial LM head), the mismatching words against the CPU oracle on
+sampled rows, and the CPU oracle timed on the host cores.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
+HBM_PEAK_GBS = 8000.0
+
+
+def _events_time(fn, steps, warmup, torch):
+    """Average ms per call of `fn` over `steps` timed calls on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        fn()
+    e1.record(s)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _rows(m, count=8):
+    return np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m).choice(m, count - 2, replace=False)]))
+
+
+def _mismatch(got, want):
+    return int(np.count_nonzero(np.ascontiguousarray(got).view(np.uint32) != np.ascontiguousarray(want).view(np.uint32)))
+
+
+def bench_prefill(torch, D, W, O, steps, warmup, check):
+    x, w, bias = W.prefill()
+    dev = "cuda:0"
+    tx, tw, tb = (torch.from_numpy(v).to(dev) for v in (x, w, bias))
+    out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=dev)
+    fn = lambda: D.gemm(tx, tw, bias=tb, out=out)  # noqa: E731
+    ms = _events_time(fn, steps, warmup, torch)
+    m, k = x.shape
+    n = w.shape[1]
+    res = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+    if check:
+        rows = _rows(m)
+        want = O.nan_canon(O.bias(O.gemm_fast(x[rows], w, 0), bias))
+        res["mismatched_words"] = _mismatch(out.cpu().numpy()[rows], want)
+        res["checked_cells"] = int(rows.size * n)
+    return res
+
+
+def bench_gemm_generic(torch, D, a, b, steps, warmup, kind="f32", O=None, check_rows=None, want_fn=None):
+    dev = "cuda:0"
+    ta = torch.from_numpy(a).to(dev)
+    if kind == "bf16":
+        tb = torch.from_numpy(b.view(np.int16)).to(dev)
+        fn = lambda: D.gemm_bf16w(ta, tb, out=out)  # noqa: E731
+    else:
+        tb = torch.from_numpy(b).to(dev)
+        fn = lambda: D.gemm(ta, tb, out=out)  # noqa: E731
+    m, k = a.shape
+    n = b.shape[1]
+    out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    ms = _events_time(fn, steps, warmup, torch)
+    res = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+    if want_fn is not None:
+        rows = check_rows if check_rows is not None else _rows(m)
+        res["mismatched_words"] = _mismatch(out.cpu().numpy()[rows], want_fn(rows))
+        res["checked_cells"] = int(len(rows) * n)
+    return res
+
+
+def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8):
+    """int8-weight GEMV; `nbuf` distinct weight buffers (> 256 MB Infinity Cache) rotate so W
+    comes from HBM.  GB/s counts K*N int8 codes + N scales + M*K x + M*N y."""
+    x16, codes, scales = W.decode()
+    x = np.ascontiguousarray(x16[:m])
+    dev = "cuda:0"
+    tx = torch.from_numpy(x).to(dev)
+    tcodes = [torch.from_numpy(codes).to(dev)] + [torch.from_numpy(np.roll(codes, i, axis=1)).to(dev)
+                                                  for i in range(1, nbuf)]
+    ts = torch.from_numpy(scales).to(dev)
+    k, n = codes.shape
+    out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    it = [0]
+
+    def fn():
+        D.gemm_int8w(tx, tcodes[it[0] % nbuf], ts, out=out)
+        it[0] += 1
+
+    ms = _events_time(fn, max(steps, nbuf), warmup, torch)
+    nbytes = k * n + 4 * n + 4 * m * k + 4 * m * n
+    res = {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
+           "bytes": nbytes}
+    if check:
+        D.gemm_int8w(tx, tcodes[0], ts, out=out)
+        want = O.gemm_fast(x, O.int8_dequant(codes, scales, 0), 0)
+        res["mismatched_words"] = _mismatch(out.cpu().numpy(), want)
+        res["checked_cells"] = int(m * n)
+    return res
+
+
+def cpu_baseline(W, O, seconds=10.0):
+    """The CPU oracle's fast arm (AVX2 FMA, all host threads) on the prefill workload's first
+    rows, grown until the run takes about `seconds`; GFLOP/s of the same arithmetic."""
+    x, w, bias = W.prefill()
+    threads = O.max_threads()
+    rows = 4
+    while True:
+        t0 = time.perf_counter()
+        y = O.gemm_fast(x[:rows], w, 0, threads=threads)
+        O.bias(y, bias)
+        dt = time.perf_counter() - t0
+        if dt * 2 > seconds or rows >= 512:
+            break
+        rows *= 2
+    n, k = w.shape[1], w.shape[0]
+    return {"value": 2.0 * rows * n * k / dt / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"prefill rows 0..{rows - 1} of 2048 (X[{rows}x4096] . W[4096x4096] + bias), "
+                      f"oracle/gemm_oracle.c fast arm, {threads} threads, {dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--all", action="store_true", help="also measure the other four workloads")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-check", action="store_true", help="skip the oracle comparison")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the product shards by output columns with no arithmetic exchange; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from mojolearn_amd import device as D
+    from mojolearn_amd import workloads as W
+    from oracle import oracle as O
+
+    check = not args.no_check
+    pre = bench_prefill(torch, D, W, O, args.steps, args.warmup, check)
+    extra = {}
+    if args.all:
+        a, b = W.gemm512()
+        extra["gemm512"] = bench_gemm_generic(torch, D, a, b, args.steps, args.warmup,
+                                              want_fn=(lambda r: O.gemm(a[r], b, 0)) if check else None)
+        for m in (1, 4, 16):
+            extra[f"decode_m{m}"] = bench_decode(torch, D, W, O, m, args.steps, args.warmup, check)
+        x, wb = W.swiglu_up()
+        extra["swiglu_up"] = bench_gemm_generic(
+            torch, D, x, wb, max(3, args.steps // 4), 1, kind="bf16",
+            want_fn=(lambda r: O.gemm_fast(x[r], O.bf16_widen(wb), 0)) if check else None)
+        x, w = W.lm_head()
+        extra["lm_head"] = bench_gemm_generic(
+            torch, D, x, w, max(3, args.steps // 2), 1,
+            want_fn=(lambda r: O.nan_canon(O.gemm_fast(x[r], w, 0))) if check else None)
+
+    line = {
+        "metric": "identical-mode FP32 GEMM TFLOP/s & % of peak; GEMV GB/s; 0 mismatched bits",
+        "value": round(pre["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (numpy PCG64 seed 1: X~N(0,1), W~N(0,0.02), bias~N(0,0.01))",
+        "config": {"workload": "prefill projection X[2048x4096] . W[4096x4096] + bias[4096], "
+                               "identical mode (fp32.v1), OP_NN",
+                   "m": 2048, "n": 4096, "k": 4096, "parallelism": "none (1 GPU)"},
+        "pct_of_peak": round(100.0 * pre["tflops"] / FP32_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 3), "peak": FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(pre["tflops"] / FP32_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    if check:
+        line["mismatched_words"] = pre["mismatched_words"]
+        line["checked_cells"] = pre["checked_cells"]
+    if extra:
+        line["workloads"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                             for k, v in extra.items()}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(W, O)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,99 @@
+/*
+ * mlgemm.h -- C ABI of libmlgemm.so, the MI355X (gfx950) implementation of
+ * mojolearn's identical-mode FP32 GEMM, profile mojolearn.identical.gemm.fp32.v1.
+ *
+ * Plain pointers and sizes only.  All functions are thread-safe; errors are reported
+ * through the sink (linalg_native_v1) or mlg_last_error() (device entries).
+ */
+#ifndef MLGEMM_H
+#define MLGEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error sink of the native op table: (context, UTF-8 message pointer, byte length).
+ * Replaces the reference's NativeDescriptorError, core/native_descriptor_abi.mojo:7-10. */
+typedef void (*mlg_sink_t)(int64_t ctx, int64_t utf8_ptr, int64_t len);
+
+/*
+ * The op table entry, same signature, op numbering and error protocol as the reference's
+ * `linalg_native_v1` (gemm/linalg_dispatch.mojo:78-89, ops :14-75).  All addresses are HOST
+ * pointers owned by the caller, row-major and contiguous; the call uploads, computes,
+ * downloads (NaN words canonicalized to 0x7FC00000) and drains before it returns.
+ * Returns 0 and writes *(int64_t*)result, or calls sink(err_ctx, msg, len) once and
+ * returns 1.  `floats`/`n_floats` must be 0 (as in the reference).
+ *
+ *   op  addrs                       ints                       result
+ *   0   [c, a, b]                   [m, n, k, op]              m*n      gemm (gemm/linalg_native.mojo:170-197)
+ *   1   [c, a, b_u16]               [m, n, k, op, a_bf16]      m*n      gemm_bf16 (gemm/linalg_native.mojo:199-256)
+ *   8   [out_u16, x_f32]            [count]                    count    to_bf16 (L-2)
+ *   9   [out_f32, bits_u16]         [count]                    count    from_bf16 (L-1)
+ *   11  []                          []                         1        numeric mode (identical)
+ *   12  []                          []                         1        fp32 profile version
+ *   13  []                          []                         1        low-bit profile version
+ *   14  []                          []                         1        int15 profile version
+ *   Extensions of this build (no reference op; numbered after the reference's 0-14):
+ *   15  [c, a, codes_i8, scales]    [m, n, k, op]              m*n      int8 weight x fp32 per-output-
+ *                                                                       channel scale: B_eff[p,j] =
+ *                                                                       ftz(f32(code) * ftz(scale[j]))
+ *   16  [c, a, b, bias]             [m, n, k, op]              m*n      gemm then nn.Linear bias,
+ *                                                                       Y = ftz(ftz(C) + ftz(bias[j]))
+ *                                                                       (transformer/impl/llama/
+ *                                                                       modeling_llama.mojo:3979-3989)
+ * Ops 2-7 and 10 (int8i32 / int15i64 profiles, from_f16) are refused by name.
+ */
+int64_t linalg_native_v1(int64_t op, int64_t addrs, int64_t n_addrs, int64_t ints, int64_t n_ints,
+                         int64_t floats, int64_t n_floats, int64_t result, int64_t err_ctx,
+                         mlg_sink_t sink);
+
+/* The ABI name the reference wraps in its PyCapsule ("mojolearn.linalg.v1",
+ * gemm/linalg_dispatch.mojo:10). */
+const char* mlg_abi_name(void);
+
+/*
+ * Device-pointer entries (the model for them: the reference's device-level
+ * identical_gemm_into / identical_gemm_leaf_ptr_into, gemm/checks/gemm_identical.mojo:6062-6144,
+ * gemm/neural_dispatch.mojo:245-320).  All buffers are DEVICE pointers (e.g. PyTorch-ROCm
+ * data_ptr()), row-major and contiguous in the layout of `op` (0 NN, 1 NT, 2 TN).  The
+ * work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and the call
+ * returns without waiting.  `bias` may be NULL.  `leaf` is the k-leaf size; 0 selects
+ * the contract's (gemm/contract.mojo:173-214), k selects the one-chain sequence-executor
+ * word (gemm/neural_dispatch.mojo:245-320).  Output NaN words are 0x7FC00000.
+ * Return 0 on success; otherwise mlg_last_error() holds the message.
+ */
+int mlg_gemm_f32(float* c, const float* a, const float* b, const float* bias, int64_t m,
+                 int64_t n, int64_t k, int32_t op, int64_t leaf, void* stream);
+
+/* bf16-stored B (and optionally A): widened exactly (bits << 16) at the tile load
+ * (bf16f32.v1, gemm/IDENTICAL_LOWBIT_CONTRACT.md L-1; reference device entry
+ * identical_gemm_bf16w_into, gemm/checks/gemm_lowbit.mojo:369-395). */
+int mlg_gemm_bf16w(float* c, const void* a, const uint16_t* b, const float* bias, int64_t m,
+                   int64_t n, int64_t k, int32_t op, int32_t a_is_bf16, int64_t leaf, void* stream);
+
+/* int8-stored B with one fp32 scale per output column j (this build's extension; the
+ * reference's int8 rows use power-of-two exponents, checks/numerics.mojo:1665-1671):
+ * B_eff[p,j] = ftz(f32(code[p,j]) * ftz(scales[j])), dequantized in the tile load. */
+int mlg_gemm_int8w(float* c, const float* a, const int8_t* codes, const float* scales,
+                   const float* bias, int64_t m, int64_t n, int64_t k, int32_t op, int64_t leaf,
+                   void* stream);
+
+/* L-1 / L-2 conversions on device buffers (checks/numerics.mojo:1548-1574). */
+int mlg_bf16_widen(float* out, const uint16_t* in, int64_t count, void* stream);
+int mlg_bf16_narrow(uint16_t* out, const float* in, int64_t count, void* stream);
+
+/* The message of the calling thread's last failed mlg_* call ("" if none). */
+const char* mlg_last_error(void);
+
+/* Profile metadata: 1 = identical; fp32 profile version; low-bit profile version. */
+int64_t mlg_numeric_mode(void);
+int64_t mlg_profile_version(void);
+int64_t mlg_lowbit_profile_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLGEMM_H */

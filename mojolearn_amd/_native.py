@@ -1,0 +1,88 @@
+"""Loader of libmlgemm.so (the gfx950 kernels behind a C ABI, include/mlgemm.h).
+
+There is no fallback: if the library is missing or cannot load, every call raises.
+"""
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmlgemm.so")
+
+_lock = threading.Lock()
+_lib = None
+
+SINK_T = ctypes.CFUNCTYPE(None, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64)
+
+
+def lib():
+    """The loaded libmlgemm.so, with argument types declared."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"mojolearn_amd: {LIB_PATH} is not built; run `python -c \"import __graft_entry__ as g; g.build()\"` "
+                "or `python mojolearn_amd/build.py` (hipcc, gfx950)")
+        L = ctypes.CDLL(LIB_PATH)
+        i64, i32, vp = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
+        L.linalg_native_v1.argtypes = [i64, i64, i64, i64, i64, i64, i64, i64, i64, SINK_T]
+        L.linalg_native_v1.restype = i64
+        L.mlg_abi_name.argtypes = []
+        L.mlg_abi_name.restype = ctypes.c_char_p
+        L.mlg_gemm_f32.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i64, vp]
+        L.mlg_gemm_f32.restype = ctypes.c_int
+        L.mlg_gemm_bf16w.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, vp]
+        L.mlg_gemm_bf16w.restype = ctypes.c_int
+        L.mlg_gemm_int8w.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, i64, vp]
+        L.mlg_gemm_int8w.restype = ctypes.c_int
+        L.mlg_bf16_widen.argtypes = [vp, vp, i64, vp]
+        L.mlg_bf16_widen.restype = ctypes.c_int
+        L.mlg_bf16_narrow.argtypes = [vp, vp, i64, vp]
+        L.mlg_bf16_narrow.restype = ctypes.c_int
+        L.mlg_last_error.argtypes = []
+        L.mlg_last_error.restype = ctypes.c_char_p
+        for name in ("mlg_numeric_mode", "mlg_profile_version", "mlg_lowbit_profile_version"):
+            getattr(L, name).argtypes = []
+            getattr(L, name).restype = i64
+        _lib = L
+    return _lib
+
+
+class NativeError(Exception):
+    pass
+
+
+def call(op, addrs, ints):
+    """One call of the op table entry `linalg_native_v1` (host pointers).
+
+    Errors come back through the sink exactly once; a message that starts with
+    "TypeError: " raises TypeError (prefix removed), anything else RuntimeError.
+    """
+    L = lib()
+    msgs = []
+
+    def _sink(ctx, ptr, n):
+        msgs.append(ctypes.string_at(ptr, n).decode("utf-8", "replace"))
+
+    sink = SINK_T(_sink)
+    a = (ctypes.c_int64 * max(len(addrs), 1))(*[int(x) for x in addrs])
+    p = (ctypes.c_int64 * max(len(ints), 1))(*[int(x) for x in ints])
+    result = ctypes.c_int64(0)
+    rc = L.linalg_native_v1(op, ctypes.addressof(a), len(addrs), ctypes.addressof(p), len(ints),
+                            0, 0, ctypes.addressof(result), 0, sink)
+    if rc != 0:
+        msg = msgs[0] if msgs else "linalg native ABI: failed without a message"
+        if msg.startswith("TypeError: "):
+            raise TypeError(msg[len("TypeError: "):])
+        raise RuntimeError(msg)
+    return result.value
+
+
+def check(rc):
+    """Raise RuntimeError with mlg_last_error() if a device entry failed."""
+    if rc != 0:
+        raise RuntimeError(lib().mlg_last_error().decode("utf-8", "replace"))

@@ -1,0 +1,335 @@
+// C ABI of libmlgemm.so (declared in include/mlgemm.h).
+//
+// linalg_native_v1 restates the reference's op table and error protocol
+// (gemm/linalg_dispatch.mojo:14-102, core/native_descriptor_call.mojo:8-13,38-55,95-100):
+// host pointers in, host pointers out, synchronous, one sink call on failure.  The
+// device-pointer entries enqueue on a caller's stream and return.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <atomic>
+#include <functional>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/mlgemm.h"
+#include "contract.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int64_t PROFILE_VERSION = 1;         // gemm/contract.mojo:140-151 (fp32.v1)
+constexpr int64_t LOWBIT_PROFILE_VERSION = 1;  // gemm/contract.mojo:397
+constexpr int64_t INT15_PROFILE_VERSION = 1;   // gemm/contract.mojo:406
+constexpr int64_t NUMERIC_MODE_IDENTICAL = 1;
+
+thread_local std::string g_last_error;
+
+struct Fail : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    throw Fail(std::string("mlgemm: ") + what + " failed: " + hipGetErrorString(e));
+}
+
+int num_cus_of_current_device() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int cus = 0;
+    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+              "hipDeviceGetAttribute");
+    cache[dev] = cus > 0 ? cus : 1;
+  }
+  return cache[dev];
+}
+
+// Enqueue one product on `stream`; the group-root workspace (if any) is allocated from
+// the stream-ordered pool and released on the same stream, so calls on different
+// streams never share it.
+void enqueue_gemm(const mlg::GemmProblem& p, hipStream_t stream) {
+  if (p.m < 0 || p.n < 0 || p.k < 0) throw Fail("mlgemm: m, n and k must be >= 0");
+  if (p.op != mlg::OP_NN && p.op != mlg::OP_NT && p.op != mlg::OP_TN)
+    throw Fail("mlgemm: op must be 0 (OP_NN), 1 (OP_NT) or 2 (OP_TN), got " + std::to_string(p.op));
+  if (p.leaf < 0) throw Fail("mlgemm: leaf must be >= 0 (0 = the contract's leaf size)");
+  if (p.m == 0 || p.n == 0) return;
+  if (!p.c || (p.k > 0 && (!p.a || !p.b))) throw Fail("mlgemm: null operand pointer");
+  if (p.b_type == mlg::T_I8 && p.k > 0 && !p.scales) throw Fail("mlgemm: int8 weight needs scales");
+  const int cus = num_cus_of_current_device();
+  const int64_t wsf = mlg::gemm_workspace_floats(p, cus);
+  float* ws = nullptr;
+  if (wsf > 0) hip_check(hipMallocAsync((void**)&ws, (size_t)wsf * sizeof(float), stream), "hipMallocAsync");
+  hipError_t e = mlg::run_gemm(p, ws, cus, stream);
+  if (ws) {
+    hipError_t f = hipFreeAsync(ws, stream);
+    if (e == hipSuccess) e = f;
+  }
+  hip_check(e, "gemm launch");
+}
+
+int guarded(const std::function<void()>& fn) {
+  try {
+    fn();
+    g_last_error.clear();
+    return 0;
+  } catch (const std::exception& ex) {
+    g_last_error = ex.what();
+    return 1;
+  }
+}
+
+// ---- host-pointer transport (the role of gemm/host_entry.mojo:79-197 and
+// gemm/host_transport.mojo:107-272): pooled device buffers guarded by a busy flag; a
+// concurrent second caller gets fresh buffers.
+struct DeviceBuf {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  void* get(size_t bytes) {
+    if (bytes == 0) bytes = 1;
+    if (bytes > cap) {
+      if (ptr) hip_check(hipFree(ptr), "hipFree");
+      ptr = nullptr;
+      cap = 0;
+      hip_check(hipMalloc(&ptr, bytes), "hipMalloc");
+      cap = bytes;
+    }
+    return ptr;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    cap = 0;
+  }
+};
+
+struct HostPool {
+  DeviceBuf c, a, b, x;
+  hipStream_t stream = nullptr;
+};
+
+std::atomic<int> g_pool_busy{0};
+HostPool g_pool;
+std::mutex g_pool_init;
+
+struct Lease {
+  HostPool* pool;
+  HostPool fresh;
+  bool pooled;
+  Lease() {
+    int expect = 0;
+    pooled = g_pool_busy.compare_exchange_strong(expect, 1);
+    if (pooled) {
+      std::lock_guard<std::mutex> lock(g_pool_init);
+      if (!g_pool.stream) hip_check(hipStreamCreateWithFlags(&g_pool.stream, hipStreamNonBlocking), "hipStreamCreate");
+      pool = &g_pool;
+    } else {
+      hip_check(hipStreamCreateWithFlags(&fresh.stream, hipStreamNonBlocking), "hipStreamCreate");
+      pool = &fresh;
+    }
+  }
+  ~Lease() {
+    if (pooled) {
+      g_pool_busy.store(0);
+    } else {
+      fresh.c.release(); fresh.a.release(); fresh.b.release(); fresh.x.release();
+      if (fresh.stream) (void)hipStreamDestroy(fresh.stream);
+    }
+  }
+};
+
+void up(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  if (bytes) hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s), "hipMemcpy H2D");
+}
+void down(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  if (bytes) hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "hipMemcpy D2H");
+}
+
+std::string shape_text(int64_t m, int64_t n, int64_t k) {
+  return "m=" + std::to_string(m) + " n=" + std::to_string(n) + " k=" + std::to_string(k);
+}
+
+// gemm/host_entry.mojo:115-126: degenerate shapes are refused at the host surface.
+void refuse_host_shape(const char* who, int64_t m, int64_t n, int64_t k, int64_t op) {
+  if (m <= 0 || n <= 0 || k <= 0)
+    throw Fail(std::string(who) + ": m, n and k must all be positive, got " + shape_text(m, n, k) +
+               " (contract section 8 specifies the degenerate shapes; this surface has no gate on"
+               " them and refuses rather than guesses)");
+  if (op != mlg::OP_NN && op != mlg::OP_NT && op != mlg::OP_TN)
+    throw Fail(std::string(who) + ": op must be 0 (OP_NN), 1 (OP_NT) or 2 (OP_TN), got " +
+               std::to_string(op));
+}
+
+int64_t host_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr, int a_type,
+                  int b_type, bool with_bias) {
+  const int64_t m = pr[0], n = pr[1], k = pr[2], op = pr[3];
+  const char* who = b_type == mlg::T_BF16 ? "gemm_bf16" : (b_type == mlg::T_I8 ? "gemm_int8w" : "identical_gemm_host");
+  refuse_host_shape(who, m, n, k, op);
+  Lease lease;
+  HostPool& P = *lease.pool;
+  const size_t ea = a_type == mlg::T_F32 ? 4 : 2;
+  const size_t eb = b_type == mlg::T_F32 ? 4 : (b_type == mlg::T_BF16 ? 2 : 1);
+  void* dc = P.c.get((size_t)(m * n) * 4);
+  void* da = P.a.get((size_t)(m * k) * ea);
+  void* db = P.b.get((size_t)(n * k) * eb);
+  float* dx = nullptr;
+  if (b_type == mlg::T_I8 || with_bias) dx = (float*)P.x.get((size_t)n * 4);
+  up(da, (const void*)ad[1], (size_t)(m * k) * ea, P.stream);
+  up(db, (const void*)ad[2], (size_t)(n * k) * eb, P.stream);
+  if (dx) up(dx, (const void*)ad[3], (size_t)n * 4, P.stream);
+  mlg::GemmProblem p{};
+  p.c = (float*)dc; p.a = da; p.b = db;
+  p.scales = b_type == mlg::T_I8 ? dx : nullptr;
+  p.bias = with_bias ? dx : nullptr;
+  p.m = m; p.n = n; p.k = k; p.op = (int)op; p.a_type = a_type; p.b_type = b_type; p.leaf = 0;
+  enqueue_gemm(p, P.stream);
+  down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  return m * n;
+}
+
+int64_t host_convert(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr, bool narrow) {
+  const char* who = narrow ? "to_bf16" : "from_bf16";
+  if (pr.size() != 1) throw Fail(std::string(who) + ": params must contain 1 value (count), got " + std::to_string(pr.size()));
+  const int64_t count = pr[0];
+  if (count <= 0) throw Fail(std::string(who) + ": count must be positive, got " + std::to_string(count));
+  Lease lease;
+  HostPool& P = *lease.pool;
+  void* dout = P.c.get((size_t)count * (narrow ? 2 : 4));
+  void* din = P.a.get((size_t)count * (narrow ? 4 : 2));
+  up(din, (const void*)ad[1], (size_t)count * (narrow ? 4 : 2), P.stream);
+  if (narrow) hip_check(mlg::run_bf16_narrow((uint16_t*)dout, (const float*)din, count, P.stream), "to_bf16 launch");
+  else hip_check(mlg::run_bf16_widen((float*)dout, (const uint16_t*)din, count, P.stream), "from_bf16 launch");
+  down((void*)ad[0], dout, (size_t)count * (narrow ? 2 : 4), P.stream);
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  return count;
+}
+
+std::vector<int64_t> words(int64_t addr, int64_t n) {
+  if (n < 0 || (n > 0 && addr == 0)) throw Fail("linalg native ABI: invalid descriptor span");
+  std::vector<int64_t> v((size_t)n);
+  if (n) memcpy(v.data(), (const void*)addr, (size_t)n * sizeof(int64_t));
+  return v;
+}
+
+int64_t native_operation(int64_t op, const std::vector<int64_t>& a, const std::vector<int64_t>& p) {
+  switch (op) {
+    case 0:
+      if (a.size() != 3) throw Fail("linalg native ABI: invalid gemm address count");
+      if (p.size() != 4) throw Fail("gemm: params must contain 4 values (m, n, k, op), got " + std::to_string(p.size()));
+      return host_gemm(a, p, mlg::T_F32, mlg::T_F32, false);
+    case 1: {
+      if (a.size() != 3) throw Fail("linalg native ABI: invalid gemm_bf16 address count");
+      if (p.size() != 5)
+        throw Fail("gemm_bf16: params must contain 5 values (m, n, k, op, a_bf16), got " + std::to_string(p.size()));
+      std::vector<int64_t> p4(p.begin(), p.begin() + 4);
+      return host_gemm(a, p4, p[4] != 0 ? mlg::T_BF16 : mlg::T_F32, mlg::T_BF16, false);
+    }
+    case 8:
+      if (a.size() != 2) throw Fail("linalg native ABI: invalid to_bf16 address count");
+      return host_convert(a, p, true);
+    case 9:
+      if (a.size() != 2) throw Fail("linalg native ABI: invalid from_bf16 address count");
+      return host_convert(a, p, false);
+    case 11:
+    case 12:
+    case 13:
+    case 14:
+      if (!a.empty() || !p.empty()) throw Fail("linalg native ABI: metadata takes no descriptors");
+      return op == 11 ? NUMERIC_MODE_IDENTICAL
+                      : (op == 12 ? PROFILE_VERSION : (op == 13 ? LOWBIT_PROFILE_VERSION : INT15_PROFILE_VERSION));
+    case 15:
+      if (a.size() != 4) throw Fail("linalg native ABI: invalid gemm_int8w address count");
+      if (p.size() != 4) throw Fail("gemm_int8w: params must contain 4 values (m, n, k, op), got " + std::to_string(p.size()));
+      return host_gemm(a, p, mlg::T_F32, mlg::T_I8, false);
+    case 16:
+      if (a.size() != 4) throw Fail("linalg native ABI: invalid gemm_bias address count");
+      if (p.size() != 4) throw Fail("gemm_bias: params must contain 4 values (m, n, k, op), got " + std::to_string(p.size()));
+      return host_gemm(a, p, mlg::T_F32, mlg::T_F32, true);
+    case 2: case 3: case 4: case 5: case 6: case 7: case 10:
+      throw Fail("linalg native ABI: operation " + std::to_string(op) +
+                 " (int8i32 / int15i64 profiles, from_f16) is not part of this build's identical fp32 GEMM path");
+    default:
+      throw Fail("linalg native ABI: unknown operation");
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t linalg_native_v1(int64_t op, int64_t addrs, int64_t n_addrs, int64_t ints, int64_t n_ints,
+                         int64_t floats, int64_t n_floats, int64_t result, int64_t err_ctx,
+                         mlg_sink_t sink) {
+  (void)floats;
+  try {
+    if (result == 0 || n_floats != 0) throw Fail("linalg native ABI: invalid result or scalar span");
+    std::vector<int64_t> a = words(addrs, n_addrs);
+    std::vector<int64_t> p = words(ints, n_ints);
+    *(int64_t*)result = native_operation(op, a, p);
+    return 0;
+  } catch (const std::exception& ex) {
+    if (sink) {
+      const std::string msg = ex.what();
+      sink(err_ctx, (int64_t)(uintptr_t)msg.data(), (int64_t)msg.size());
+    }
+    return 1;
+  }
+}
+
+const char* mlg_abi_name(void) { return "mojolearn.linalg.v1"; }
+
+int mlg_gemm_f32(float* c, const float* a, const float* b, const float* bias, int64_t m, int64_t n,
+                 int64_t k, int32_t op, int64_t leaf, void* stream) {
+  return guarded([&] {
+    mlg::GemmProblem p{};
+    p.c = c; p.a = a; p.b = b; p.bias = bias; p.m = m; p.n = n; p.k = k; p.op = op;
+    p.a_type = mlg::T_F32; p.b_type = mlg::T_F32; p.leaf = leaf;
+    enqueue_gemm(p, (hipStream_t)stream);
+  });
+}
+
+int mlg_gemm_bf16w(float* c, const void* a, const uint16_t* b, const float* bias, int64_t m,
+                   int64_t n, int64_t k, int32_t op, int32_t a_is_bf16, int64_t leaf, void* stream) {
+  return guarded([&] {
+    mlg::GemmProblem p{};
+    p.c = c; p.a = a; p.b = b; p.bias = bias; p.m = m; p.n = n; p.k = k; p.op = op;
+    p.a_type = a_is_bf16 ? mlg::T_BF16 : mlg::T_F32; p.b_type = mlg::T_BF16; p.leaf = leaf;
+    enqueue_gemm(p, (hipStream_t)stream);
+  });
+}
+
+int mlg_gemm_int8w(float* c, const float* a, const int8_t* codes, const float* scales,
+                   const float* bias, int64_t m, int64_t n, int64_t k, int32_t op, int64_t leaf,
+                   void* stream) {
+  return guarded([&] {
+    mlg::GemmProblem p{};
+    p.c = c; p.a = a; p.b = codes; p.scales = scales; p.bias = bias; p.m = m; p.n = n; p.k = k;
+    p.op = op; p.a_type = mlg::T_F32; p.b_type = mlg::T_I8; p.leaf = leaf;
+    enqueue_gemm(p, (hipStream_t)stream);
+  });
+}
+
+int mlg_bf16_widen(float* out, const uint16_t* in, int64_t count, void* stream) {
+  return guarded([&] { hip_check(mlg::run_bf16_widen(out, in, count, (hipStream_t)stream), "from_bf16 launch"); });
+}
+
+int mlg_bf16_narrow(uint16_t* out, const float* in, int64_t count, void* stream) {
+  return guarded([&] { hip_check(mlg::run_bf16_narrow(out, in, count, (hipStream_t)stream), "to_bf16 launch"); });
+}
+
+const char* mlg_last_error(void) { return g_last_error.c_str(); }
+
+int64_t mlg_numeric_mode(void) { return NUMERIC_MODE_IDENTICAL; }
+int64_t mlg_profile_version(void) { return PROFILE_VERSION; }
+int64_t mlg_lowbit_profile_version(void) { return LOWBIT_PROFILE_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,118 @@
+"""Device-resident entry points on PyTorch-ROCm tensors (torch is plumbing: device memory
+and streams).  These are the model-code entries -- the role of the reference's
+identical_gemm_into / GemmWorkspace.run (gemm/checks/gemm_identical.mojo:6062-6144,
+gemm/neural_dispatch.mojo:468-478) -- enqueued on the current torch stream, no copies.
+"""
+import torch
+
+from . import _native
+
+OP_NN, OP_NT, OP_TN = 0, 1, 2
+
+
+def _shape(a, b, op):
+    if op == OP_NN:
+        (m, k), (kb, n) = a.shape, b.shape
+    elif op == OP_NT:
+        (m, k), (n, kb) = a.shape, b.shape
+    elif op == OP_TN:
+        (k, m), (kb, n) = a.shape, b.shape
+    else:
+        raise ValueError(f"op must be 0 (OP_NN), 1 (OP_NT) or 2 (OP_TN), got {op}")
+    if k != kb:
+        raise ValueError(f"contracted extents differ: a gives k={k}, b gives k={kb}")
+    return m, n, k
+
+
+def _check(t, name, dtype):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} has dtype {t.dtype}, want {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _stream(t):
+    return ctypes_stream(torch.cuda.current_stream(t.device))
+
+
+def ctypes_stream(s):
+    return s.cuda_stream
+
+
+def _prep_out(out, m, n, ref):
+    if out is None:
+        return torch.empty((m, n), dtype=torch.float32, device=ref.device)
+    _check(out, "out", torch.float32)
+    if tuple(out.shape) != (m, n):
+        raise ValueError(f"out has shape {tuple(out.shape)}, want ({m}, {n})")
+    return out
+
+
+def _bias(bias, n):
+    if bias is None:
+        return None
+    _check(bias, "bias", torch.float32)
+    if bias.numel() != n:
+        raise ValueError(f"bias must hold n={n} values")
+    return bias.data_ptr()
+
+
+def gemm(a, b, *, op=OP_NN, bias=None, out=None, leaf=0):
+    """C = op(a) . op(b) (fp32.v1), optional fused nn.Linear bias.  float32 tensors."""
+    _check(a, "a", torch.float32)
+    _check(b, "b", torch.float32)
+    m, n, k = _shape(a, b, op)
+    c = _prep_out(out, m, n, a)
+    with torch.cuda.device(a.device):
+        _native.check(_native.lib().mlg_gemm_f32(c.data_ptr(), a.data_ptr(), b.data_ptr(), _bias(bias, n),
+                                                 m, n, k, op, leaf, _stream(a)))
+    return c
+
+
+def gemm_bf16w(a, b_bits, *, op=OP_NN, bias=None, out=None, leaf=0):
+    """C = op(a) . op(widen(b_bits)); b_bits is a torch.int16/uint16 tensor of bf16 bits
+    (a may be float32 or bf16 bits too)."""
+    if b_bits.dtype not in (torch.int16, torch.uint16):
+        raise TypeError("b_bits must hold bf16 bits as int16/uint16")
+    a_bits = a.dtype in (torch.int16, torch.uint16)
+    if not a_bits:
+        _check(a, "a", torch.float32)
+    m, n, k = _shape(a, b_bits, op)
+    c = _prep_out(out, m, n, a)
+    with torch.cuda.device(a.device):
+        _native.check(_native.lib().mlg_gemm_bf16w(c.data_ptr(), a.data_ptr(), b_bits.data_ptr(), _bias(bias, n),
+                                                   m, n, k, op, 1 if a_bits else 0, leaf, _stream(a)))
+    return c
+
+
+def gemm_int8w(a, codes, scales, *, op=OP_NN, bias=None, out=None, leaf=0):
+    """C = op(a) . W, W[p, j] = ftz(f32(codes[p, j]) * ftz(scales[j])) (int8 codes, one
+    float32 scale per output column)."""
+    _check(a, "a", torch.float32)
+    _check(codes, "codes", torch.int8)
+    _check(scales, "scales", torch.float32)
+    m, n, k = _shape(a, codes, op)
+    if scales.numel() != n:
+        raise ValueError(f"scales must hold n={n} values")
+    c = _prep_out(out, m, n, a)
+    with torch.cuda.device(a.device):
+        _native.check(_native.lib().mlg_gemm_int8w(c.data_ptr(), a.data_ptr(), codes.data_ptr(), scales.data_ptr(),
+                                                   _bias(bias, n), m, n, k, op, leaf, _stream(a)))
+    return c
+
+
+def bf16_widen(bits):
+    out = torch.empty(bits.shape, dtype=torch.float32, device=bits.device)
+    with torch.cuda.device(bits.device):
+        _native.check(_native.lib().mlg_bf16_widen(out.data_ptr(), bits.data_ptr(), bits.numel(), _stream(bits)))
+    return out
+
+
+def bf16_narrow(x):
+    _check(x, "x", torch.float32)
+    out = torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    with torch.cuda.device(x.device):
+        _native.check(_native.lib().mlg_bf16_narrow(out.data_ptr(), x.data_ptr(), x.numel(), _stream(x)))
+    return out

@@ -1,0 +1,311 @@
+"""Float32 bit-identical matrix product on MI355X: the surface of `mojolearn.linalg`
+for the identical fp32 GEMM path (python/mojolearn/linalg.py, _linalg_impl.py:91-415),
+backed by the gfx950 kernels of libmlgemm.so through its C op table.
+
+`matmul` computes ``op(a) @ op(b)`` under the profile ``mojolearn.identical.gemm.fp32.v1``:
+k-leaves of `contract_leaf_size(k)` accumulated serially ascending with one FMA per step,
+flush-to-zero at every seam, folded by the fixed balanced tree, NaN words canonicalized.
+The same names, operation table, refusals and exception types as the reference surface;
+argument admission restates bindings/linalg_ops_lowbit_door.mojo:259-416,654-710.
+
+Results are NumPy arrays (``numpy.asarray`` on them is the identity).
+"""
+import numpy as np
+
+from . import _native
+
+PROFILE_FAMILY = "mojolearn.identical.gemm.fp32"
+PROFILE_VERSION = 1
+PROFILE = f"{PROFILE_FAMILY}.v{PROFILE_VERSION}"
+LOWBIT_PROFILE_VERSION = 1
+PROFILE_BF16 = f"mojolearn.identical.gemm.bf16f32.v{LOWBIT_PROFILE_VERSION}"
+#: This build's int8-weight extension: int8 codes times one float32 scale per output
+#: column, dequantized exactly as ftz(f32(code) * ftz(scale)) and then fp32.v1.
+PROFILE_INT8W = "mojolearn.identical.gemm.int8w-colscale-f32.v1"
+
+OP_NN, OP_NT, OP_TN = 0, 1, 2
+
+# op codes of the native table (gemm/linalg_dispatch.mojo:14-75, + this build's 15, 16)
+_LIN_OP_GEMM = 0
+_LIN_OP_GEMM_BF16 = 1
+_LIN_OP_TO_BF16 = 8
+_LIN_OP_FROM_BF16 = 9
+_LIN_OP_MODE = 11
+_LIN_OP_PROFILE_VERSION = 12
+_LIN_OP_LOWBIT_VERSION = 13
+_LIN_OP_GEMM_INT8W = 15
+_LIN_OP_GEMM_BIAS = 16
+
+
+def _shape_text(shape):
+    return "(" + ", ".join(str(int(s)) for s in shape) + ("," if len(shape) == 1 else "") + ")"
+
+
+def _dtype_name(x):
+    return str(x.dtype)
+
+
+def _asarray(x):
+    return x if isinstance(x, np.ndarray) else np.asarray(x)
+
+
+def _operand(x, name):
+    """`lin_operand`: a float32 2-D buffer, refused by name otherwise, in C order (a layout
+    copy at most, never a cast).  bindings/linalg_ops_lowbit_door.mojo:259-296."""
+    v = _asarray(x)
+    if v.dtype != np.float32:
+        raise TypeError(
+            f"mojolearn.linalg: {name} has dtype {_dtype_name(v)}, and only float32 is in this profile "
+            f"({PROFILE}; contract section 1 makes FP32 a hard requirement, and section 0.5 excludes FP16, "
+            "BF16, TF32 and float64). Refused rather than cast, because a cast from float64 drops mantissa "
+            f"bits you may care about. Convert it yourself with np.asarray({name}, dtype=np.float32) if that "
+            "is what you want.")
+    if v.ndim != 2:
+        raise ValueError(
+            f"mojolearn.linalg: {name} must be 2-D, got {v.ndim}-D shape {_shape_text(v.shape)}. A vector "
+            "product is OP_NT at n == 1 (contract 0.1); pass it as a 2-D array of shape (n, k) or (k, 1).")
+    if v.size == 0:
+        raise ValueError(
+            f"mojolearn.linalg: {name} has shape {_shape_text(v.shape)} and no elements. Contract section 8 "
+            "does specify the degenerate shapes (k == 0 writes +0.0 into every cell; m == 0 or n == 0 writes "
+            "nothing), but no gate in this tree has run them through the Python surface, so they are refused "
+            "here rather than answered unchecked.")
+    return np.ascontiguousarray(v)
+
+
+def _operand_bits(x, name):
+    """`lin_operand_bits`: a 2-D uint16 buffer of bf16 bits in C order (door :299-316)."""
+    v = _asarray(x)
+    if v.dtype != np.uint16:
+        raise TypeError(
+            f"mojolearn.linalg: {name} has dtype {_dtype_name(v)}; the bf16 profile takes bf16 BITS in a "
+            "uint16 buffer, which to_bf16() produces. Refused rather than reinterpreted.")
+    if v.ndim != 2:
+        raise ValueError(f"mojolearn.linalg: {name} must be 2-D, got {v.ndim}-D")
+    if v.size == 0:
+        raise ValueError(f"mojolearn.linalg: {name} has no elements")
+    return np.ascontiguousarray(v)
+
+
+def _out(out, m, n, who):
+    """`lin_out` (door :327-343): a new float32 (m, n) array, or the caller's, checked."""
+    if out is None:
+        return np.empty((m, n), dtype=np.float32)
+    if not isinstance(out, np.ndarray):
+        out = np.asarray(out)
+    if out.dtype != np.float32:
+        raise TypeError(f"mojolearn.linalg.{who}: out must be float32")
+    if out.ndim != 2 or out.shape[0] != m or out.shape[1] != n:
+        raise ValueError(f"mojolearn.linalg.{who}: out has shape {_shape_text(out.shape)}, want ({m}, {n})")
+    if not out.flags.c_contiguous or not out.flags.writeable:
+        raise ValueError(f"mojolearn.linalg.{who}: out must be C-contiguous and writable")
+    return out
+
+
+def _op_and_shape(a, b, transpose_a, transpose_b, who):
+    """`_lin_op_and_shape` (door :654-686)."""
+    ta, tb = bool(transpose_a), bool(transpose_b)
+    if ta and tb:
+        raise ValueError(
+            f"mojolearn.linalg.{who}: transpose_a and transpose_b together is not one of the contract's three "
+            "operations (section 0.1); write (b @ a).T with the flags swapped, in your own source.")
+    if ta:
+        op, (k, m), (kb, n) = OP_TN, a.shape, b.shape
+    elif tb:
+        op, (m, k), (n, kb) = OP_NT, a.shape, b.shape
+    else:
+        op, (m, k), (kb, n) = OP_NN, a.shape, b.shape
+    if k != kb:
+        raise ValueError(
+            f"mojolearn.linalg.{who}: contracted extents differ, a gives k={k} and b gives k={kb} "
+            f"(a.shape={_shape_text(a.shape)}, b.shape={_shape_text(b.shape)}, transpose_a={transpose_a}, "
+            f"transpose_b={transpose_b})")
+    return op, m, n, k
+
+
+def numeric_mode():
+    """'identical': the mode of the loaded binary, read back from it (op 11)."""
+    mode = _native.call(_LIN_OP_MODE, [], [])
+    if mode != 1:
+        raise RuntimeError(f"mojolearn.linalg: the loaded linalg binary reports numeric mode {mode}")
+    version = _native.call(_LIN_OP_PROFILE_VERSION, [], [])
+    if version != PROFILE_VERSION:
+        raise RuntimeError(
+            f"mojolearn.linalg: the loaded binary computes profile version {version}, this module "
+            f"expects {PROFILE_VERSION} ({PROFILE})")
+    return "identical"
+
+
+def profile():
+    """The matrix-product profile this process loaded, as a dict (python/mojolearn/_linalg_impl.py:170-190)."""
+    mode = numeric_mode()
+    return {
+        "profile": PROFILE,
+        "profile_family": PROFILE_FAMILY,
+        "profile_version": PROFILE_VERSION,
+        "lowbit_profile_version": _native.call(_LIN_OP_LOWBIT_VERSION, [], []),
+        "numeric_mode": mode,
+        "identity_claimed": mode == "identical",
+        "dtype": "float32",
+        "ops": ["OP_NN", "OP_NT", "OP_TN"],
+        "binary": _native.LIB_PATH,
+        "abi": _native.lib().mlg_abi_name().decode(),
+    }
+
+
+def require_identical():
+    """Raise RuntimeError unless the loaded binary is the identical build."""
+    if numeric_mode() != "identical":
+        raise RuntimeError("mojolearn.linalg: the identical build is not loaded")
+
+
+def matmul(a, b, *, transpose_a=False, transpose_b=False, out=None, identical=True):
+    """Float32 matrix product ``op(a) @ op(b)`` with the bits of ``mojolearn.identical.gemm.fp32.v1``.
+
+    ===========  ===========  ===========  ========  ========
+    transpose_a  transpose_b  C            a.shape   b.shape
+    ===========  ===========  ===========  ========  ========
+    False        False        ``a @ b``    (m, k)    (k, n)
+    False        True         ``a @ b.T``  (m, k)    (n, k)
+    True         False        ``a.T @ b``  (k, m)    (k, n)
+    ===========  ===========  ===========  ========  ========
+
+    Both True raises ValueError.  Non-float32 operands raise TypeError (never cast).
+    NaN output words are 0x7FC00000.  Restates bindings/linalg_ops_lowbit_door.mojo:347-416.
+    """
+    if identical:
+        require_identical()
+    else:
+        numeric_mode()
+    ta, tb = bool(transpose_a), bool(transpose_b)
+    if ta and tb:
+        raise ValueError(
+            f"mojolearn.linalg.matmul: transpose_a=True with transpose_b=True is refused. {PROFILE} has "
+            "exactly three operations (contract section 0.1: OP_NN, OP_NT, OP_TN) and a.T @ b.T is not one "
+            "of them. This function will not materialize a transpose to fake a fourth. If you want it, write "
+            "the identity yourself:\n    np.ascontiguousarray(np.asarray(matmul(b, a)).T)\nwhich is "
+            "(b @ a).T == a.T @ b.T, runs as OP_NN, and leaves the extra step visible in your source where "
+            "you can price it.")
+    op = OP_NN if not ta and not tb else (OP_NT if tb else OP_TN)
+    A = _operand(a, "a")
+    B = _operand(b, "b")
+    m = A.shape[1] if ta else A.shape[0]
+    k = A.shape[0] if ta else A.shape[1]
+    n = B.shape[0] if tb else B.shape[1]
+    kb = B.shape[1] if tb else B.shape[0]
+    if k != kb:
+        raise ValueError(
+            f"mojolearn.linalg.matmul: contracted extents disagree, a gives k={k} and b gives k={kb} "
+            f"(a.shape={_shape_text(A.shape)}, b.shape={_shape_text(B.shape)}, transpose_a={ta}, "
+            f"transpose_b={tb}). The row-major shapes for each op are in this function's table and in "
+            "contract section 0.1.")
+    if out is None:
+        C = np.empty((m, n), dtype=np.float32)
+    else:
+        C = out if isinstance(out, np.ndarray) else np.asarray(out)
+        if C.dtype != np.float32:
+            raise TypeError(
+                f"mojolearn.linalg.matmul: out has dtype {C.dtype}, and the profile's output is float32 "
+                "(contract section 1). Refused rather than cast on the way out.")
+        if C.ndim != 2 or C.shape[0] != m or C.shape[1] != n:
+            raise ValueError(f"mojolearn.linalg.matmul: out has shape {_shape_text(C.shape)}, want ({m}, {n})")
+        if not C.flags.c_contiguous:
+            raise ValueError(
+                "mojolearn.linalg.matmul: out must be C-contiguous; the device writes it directly (contract "
+                "section 2). A non-contiguous out cannot be written in place, and copying into it afterwards "
+                "would make `out` a lie about where the result was produced.")
+        if not C.flags.writeable:
+            raise ValueError(
+                "mojolearn.linalg.matmul: out is read-only, refusing to write to it; the device writes `out` "
+                "directly (contract section 2) and a read-only buffer handed to it is memory corruption, not "
+                "an exception.")
+    _native.call(_LIN_OP_GEMM, [C.ctypes.data, A.ctypes.data, B.ctypes.data], [m, n, k, op])
+    return C if out is None else out
+
+
+def matmul_bf16(a, b, *, transpose_a=False, transpose_b=False, out=None):
+    """Matrix product with bfloat16 operands under ``mojolearn.identical.gemm.bf16f32.v1``.
+
+    `b` is bfloat16 bits (uint16, from `to_bf16`); `a` is float32 or bfloat16 bits.  The
+    operands are widened exactly and multiplied with `matmul`'s arithmetic, so
+    ``matmul(from_bf16(a_bits), from_bf16(b_bits))`` gives the same bits.
+    """
+    require_identical()
+    av = _asarray(a)
+    a_bits = av.dtype == np.uint16
+    A = _operand_bits(av, "a") if a_bits else _operand(av, "a")
+    B = _operand_bits(b, "b")
+    op, m, n, k = _op_and_shape(A, B, transpose_a, transpose_b, "matmul_bf16")
+    C = _out(out, m, n, "matmul_bf16")
+    _native.call(_LIN_OP_GEMM_BF16, [C.ctypes.data, A.ctypes.data, B.ctypes.data], [m, n, k, op, 1 if a_bits else 0])
+    return C
+
+
+def to_bf16(x):
+    """float32 -> bfloat16 bits: flush, then round to nearest even (L-2)."""
+    v = np.ascontiguousarray(_asarray(x))
+    if v.dtype != np.float32:
+        raise TypeError(f"mojolearn.linalg.to_bf16: x has dtype {v.dtype}, want float32")
+    if v.size == 0:
+        raise ValueError("mojolearn.linalg.to_bf16: x has no elements")
+    out = np.empty(v.shape, dtype=np.uint16)
+    _native.call(_LIN_OP_TO_BF16, [out.ctypes.data, v.ctypes.data], [v.size])
+    return out
+
+
+def from_bf16(bits):
+    """bfloat16 bits (uint16) -> float32, exactly (L-1)."""
+    v = np.ascontiguousarray(_asarray(bits))
+    if v.dtype != np.uint16:
+        raise TypeError(f"mojolearn.linalg.from_bf16: bits has dtype {v.dtype}, want uint16")
+    if v.size == 0:
+        raise ValueError("mojolearn.linalg.from_bf16: bits has no elements")
+    out = np.empty(v.shape, dtype=np.float32)
+    _native.call(_LIN_OP_FROM_BF16, [out.ctypes.data, v.ctypes.data], [v.size])
+    return out
+
+
+def matmul_int8w(a, codes, scales, *, transpose_b=False, out=None):
+    """``a @ W`` with W stored as int8 codes and one float32 scale per output column.
+
+    Extension of this build (profile `PROFILE_INT8W`): ``W[p, j] = ftz(f32(codes[p, j]) *
+    ftz(scales[j]))`` -- one RNE multiply -- then fp32.v1.  `codes` is (k, n), or (n, k)
+    with ``transpose_b=True`` (the LM's ``W[out, in]`` layout).
+    """
+    require_identical()
+    A = _operand(a, "a")
+    Q = _asarray(codes)
+    if Q.dtype != np.int8:
+        raise TypeError(f"mojolearn.linalg.matmul_int8w: codes has dtype {Q.dtype}, want int8")
+    if Q.ndim != 2 or Q.size == 0:
+        raise ValueError("mojolearn.linalg.matmul_int8w: codes must be 2-D and non-empty")
+    Q = np.ascontiguousarray(Q)
+    op, m, n, k = _op_and_shape(A, Q, False, transpose_b, "matmul_int8w")
+    S = np.ascontiguousarray(_asarray(scales))
+    if S.dtype != np.float32 or S.size != n:
+        raise ValueError(f"mojolearn.linalg.matmul_int8w: scales must hold n={n} float32 values")
+    C = _out(out, m, n, "matmul_int8w")
+    _native.call(_LIN_OP_GEMM_INT8W, [C.ctypes.data, A.ctypes.data, Q.ctypes.data, S.ctypes.data], [m, n, k, op])
+    return C
+
+
+def linear(x, w, bias, *, transpose_b=False, out=None):
+    """``Y = ftz(ftz(x @ w) + ftz(bias[j]))``: the product, then the LM's nn.Linear bias
+    (transformer/impl/llama/modeling_llama.mojo:3979-3989), fused into the store."""
+    require_identical()
+    A = _operand(x, "x")
+    B = _operand(w, "w")
+    op, m, n, k = _op_and_shape(A, B, False, transpose_b, "linear")
+    bv = np.ascontiguousarray(_asarray(bias))
+    if bv.dtype != np.float32:
+        raise TypeError(f"mojolearn.linalg.linear: bias has dtype {bv.dtype}, want float32")
+    if bv.size != n:
+        raise ValueError(f"mojolearn.linalg.linear: bias must hold n={n} values")
+    C = _out(out, m, n, "linear")
+    _native.call(_LIN_OP_GEMM_BIAS, [C.ctypes.data, A.ctypes.data, B.ctypes.data, bv.ctypes.data], [m, n, k, op])
+    return C
+
+
+__all__ = ["matmul", "matmul_bf16", "matmul_int8w", "linear", "to_bf16", "from_bf16", "numeric_mode",
+           "profile", "require_identical", "PROFILE", "PROFILE_FAMILY", "PROFILE_VERSION", "PROFILE_BF16",
+           "PROFILE_INT8W", "OP_NN", "OP_NT", "OP_TN"]

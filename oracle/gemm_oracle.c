@@ -1,0 +1,348 @@
+/*
+ * CPU oracle for the profile mojolearn.identical.gemm.fp32.v1 (TEST INFRASTRUCTURE).
+ *
+ * This file is the checker, never the product: only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg load it.  The product path (mojolearn_amd) runs
+ * hand-written gfx950 HIP kernels and has no CPU fallback.
+ *
+ * It restates, in plain C, the reference's normative CPU algorithm:
+ *   - leaf rule                 gemm/contract.mojo:173-235
+ *   - orientations _a_at/_b_at  gemm/host/gemm_oracle.mojo:122-137
+ *   - leaf chain                gemm/host/gemm_oracle.mojo:146-206
+ *   - balanced fold tree        gemm/host/gemm_oracle.mojo:218-272
+ *   - gemm_oracle / _cell       gemm/host/gemm_oracle.mojo:275-371
+ *   - gemm_oracle_serial        gemm/host/gemm_oracle.mojo:473-524
+ *   - ftz (integer spelling)    checks/numerics.mojo:262-268
+ *   - bf16 widen / narrow       checks/numerics.mojo:1548-1574
+ *   - NaN canonicalization      core/nan_canon.mojo:55-130
+ *   - bias add                  transformer/impl/llama/modeling_llama.mojo:3979-3989
+ *   - card fill + FNV-1a64      bench/gemm_card_main.mojo:292-311, core/identity_trace.mojo:89-115
+ * and a fast threaded arm that computes the same bits (the role of the reference's
+ * gemm/host/gemm_host_rows.mojo:467-556): operands flushed once, columns vectorised
+ * with AVX2 FMA (one independent chain per column, so no reassociation inside a leaf),
+ * the per-step flush done as a compare+select, leaves folded with the register-stack
+ * form of the balanced tree (pushing partials in ascending order, merging with the
+ * earlier slot on the left, draining lowest level first and joining on the left).
+ *
+ * Build flags (oracle/Makefile): -O3 -mavx2 -mfma -ffp-contract=off, no fast-math,
+ * default MXCSR (no FTZ/DAZ).  fmaf() is therefore one IEEE fused multiply-add and
+ * a*b is one IEEE multiply.
+ *
+ * Pinning (tests/test_oracle_*.py): the reference's own card hashes (device card and
+ * host-capped oracle card), the verify-table gemm cells, the closed-form fixtures F1-F8
+ * of gemm/checks/gemm_oracle_check.mojo, exact-rational brute force on tiny shapes,
+ * and literal-tree == register-stack fold for P = 1..2100.
+ */
+#include <immintrin.h>
+#include <math.h>
+#include <omp.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define K_LEAF_MIN 128
+#define MAX_LEAVES 1024
+#define OP_NN 0
+#define OP_NT 1
+#define OP_TN 2
+
+static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static inline float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+/* checks/numerics.mojo:262-268: a subnormal becomes the zero of its own sign. */
+static inline float ftz(float x) {
+  uint32_t b = f2u(x);
+  if ((b & 0x7F800000u) == 0u && (b & 0x007FFFFFu) != 0u) return u2f(b & 0x80000000u);
+  return x;
+}
+
+float orc_ftz(float x) { return ftz(x); }
+float orc_fma(float a, float b, float c) { return fmaf(a, b, c); }
+
+/* gemm/contract.mojo:173-214 */
+int64_t orc_leaf_size(int64_t k) {
+  if (k <= 0) return 1;
+  if (k <= K_LEAF_MIN) return k;
+  int64_t p0 = (k + K_LEAF_MIN - 1) / K_LEAF_MIN;
+  if (p0 <= MAX_LEAVES) return K_LEAF_MIN;
+  return (k + MAX_LEAVES - 1) / MAX_LEAVES;
+}
+
+/* gemm/contract.mojo:217-226 */
+int64_t orc_leaf_count(int64_t k, int64_t leaf) {
+  if (k <= 0) return 0;
+  if (leaf < 1) leaf = 1;
+  return (k + leaf - 1) / leaf;
+}
+
+/* gemm/host/gemm_oracle.mojo:122-137 */
+static inline float a_at(const float* a, int op, int64_t i, int64_t p, int64_t m, int64_t k) {
+  return op == OP_TN ? a[p * m + i] : a[i * k + p];
+}
+static inline float b_at(const float* b, int op, int64_t p, int64_t j, int64_t n, int64_t k) {
+  return op == OP_NT ? b[j * k + p] : b[p * n + j];
+}
+
+/* gemm/host/gemm_oracle.mojo:146-206 */
+static float leaf_partial(const float* a, const float* b, int op, int64_t i, int64_t j, int64_t m,
+                          int64_t n, int64_t k, int64_t p0, int64_t p1) {
+  float acc = 0.0f;
+  for (int64_t p = p0; p < p1; ++p)
+    acc = ftz(fmaf(ftz(a_at(a, op, i, p, m, k)), ftz(b_at(b, op, p, j, n, k)), acc));
+  return ftz(acc);
+}
+
+/* gemm/host/gemm_oracle.mojo:218-272: the literal level-by-level tree.  `buf` is
+ * overwritten (it is the level being reduced in place: next[q] lands in cur[q]). */
+float orc_fold_tree(float* buf, int64_t p) {
+  if (p <= 0) return 0.0f;
+  int64_t width = p;
+  while (width > 1) {
+    int64_t pairs = width / 2;
+    for (int64_t q = 0; q < pairs; ++q) buf[q] = ftz(ftz(buf[2 * q]) + ftz(buf[2 * q + 1]));
+    if (width & 1) buf[pairs] = buf[width - 1]; /* the carry: bit for bit */
+    width = pairs + (width & 1);
+  }
+  return ftz(buf[0]);
+}
+
+/* The register-stack realisation of the same tree (what the device kernels and the
+ * fast arm use); checked against orc_fold_tree for every P in tests. */
+float orc_fold_stack(const float* parts, int64_t p) {
+  if (p <= 0) return 0.0f;
+  float slot[64];
+  uint64_t occ = 0;
+  for (int64_t t = 0; t < p; ++t) {
+    float x = parts[t];
+    int lvl = 0;
+    while (occ & (1ull << lvl)) {
+      x = ftz(ftz(slot[lvl]) + ftz(x));
+      occ &= ~(1ull << lvl);
+      ++lvl;
+    }
+    slot[lvl] = x;
+    occ |= 1ull << lvl;
+  }
+  int have = 0;
+  float r = 0.0f;
+  for (int lvl = 0; lvl < 64; ++lvl) {
+    if (!(occ & (1ull << lvl))) continue;
+    r = have ? ftz(ftz(slot[lvl]) + ftz(r)) : slot[lvl];
+    have = 1;
+  }
+  return ftz(r);
+}
+
+/* gemm/host/gemm_oracle.mojo:275-371 at an explicit leaf (0 = the contract's). */
+void orc_gemm(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int op,
+              int64_t leaf) {
+  if (leaf <= 0) leaf = orc_leaf_size(k);
+  int64_t pc = orc_leaf_count(k, leaf);
+  float* parts = (float*)malloc(sizeof(float) * (size_t)(pc > 0 ? pc : 1));
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      if (pc == 0) { c[i * n + j] = 0.0f; continue; }
+      if (pc == 1) { c[i * n + j] = ftz(leaf_partial(a, b, op, i, j, m, n, k, 0, k)); continue; }
+      for (int64_t t = 0; t < pc; ++t) {
+        int64_t e = (t + 1) * leaf;
+        if (e > k) e = k;
+        parts[t] = leaf_partial(a, b, op, i, j, m, n, k, t * leaf, e);
+      }
+      c[i * n + j] = orc_fold_tree(parts, pc);
+    }
+  free(parts);
+}
+
+/* gemm/host/gemm_oracle.mojo:473-524: one whole-k chain per cell (diagnostic). */
+void orc_gemm_serial(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k,
+                     int op) {
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) c[i * n + j] = ftz(leaf_partial(a, b, op, i, j, m, n, k, 0, k));
+}
+
+/* ---------------- fast arm: same bits, AVX2 + OpenMP ---------------- */
+
+static inline __m256 vftz(__m256 x) {
+  const __m256 sign = _mm256_castsi256_ps(_mm256_set1_epi32((int)0x80000000u));
+  const __m256 tiny = _mm256_castsi256_ps(_mm256_set1_epi32(0x00800000));
+  __m256 mag = _mm256_andnot_ps(sign, x);
+  __m256 sub = _mm256_cmp_ps(mag, tiny, _CMP_LT_OQ); /* |x| < 2^-126 (zeros map to themselves) */
+  return _mm256_blendv_ps(x, _mm256_and_ps(x, sign), sub);
+}
+
+#define FAST_VEC 4 /* 4 x 8 = 32 columns per panel */
+
+/* One row i, one panel of 32 columns starting at j0 (full panel).  ae: row of A_eff
+ * (flushed, length k), be: B_eff (flushed, k x ldb row-major). */
+static void fast_panel(float* crow, const float* ae, const float* be, int64_t ldb, int64_t j0,
+                       int64_t k, int64_t leaf, int64_t pc) {
+  __m256 slot[48][FAST_VEC];
+  uint64_t occ = 0;
+  for (int64_t t = 0; t < pc; ++t) {
+    int64_t p0 = t * leaf, p1 = p0 + leaf;
+    if (p1 > k) p1 = k;
+    __m256 acc[FAST_VEC];
+    for (int v = 0; v < FAST_VEC; ++v) acc[v] = _mm256_setzero_ps();
+    for (int64_t p = p0; p < p1; ++p) {
+      __m256 av = _mm256_set1_ps(ae[p]);
+      const float* bp = be + p * ldb + j0;
+      for (int v = 0; v < FAST_VEC; ++v) acc[v] = vftz(_mm256_fmadd_ps(av, _mm256_loadu_ps(bp + 8 * v), acc[v]));
+    }
+    int lvl = 0;
+    while (occ & (1ull << lvl)) {
+      for (int v = 0; v < FAST_VEC; ++v) acc[v] = vftz(_mm256_add_ps(slot[lvl][v], acc[v]));
+      occ &= ~(1ull << lvl);
+      ++lvl;
+    }
+    for (int v = 0; v < FAST_VEC; ++v) slot[lvl][v] = acc[v];
+    occ |= 1ull << lvl;
+  }
+  __m256 r[FAST_VEC];
+  int have = 0;
+  for (int lvl = 0; lvl < 48; ++lvl) {
+    if (!(occ & (1ull << lvl))) continue;
+    for (int v = 0; v < FAST_VEC; ++v) r[v] = have ? vftz(_mm256_add_ps(slot[lvl][v], r[v])) : slot[lvl][v];
+    have = 1;
+  }
+  for (int v = 0; v < FAST_VEC; ++v) {
+    if (!have) r[v] = _mm256_setzero_ps();
+    _mm256_storeu_ps(crow + j0 + 8 * v, vftz(r[v]));
+  }
+}
+
+/* Scalar tail column, same arithmetic. */
+static float fast_cell(const float* ae, const float* be, int64_t ldb, int64_t j, int64_t k,
+                       int64_t leaf, int64_t pc) {
+  float slot[48];
+  uint64_t occ = 0;
+  for (int64_t t = 0; t < pc; ++t) {
+    int64_t p0 = t * leaf, p1 = p0 + leaf;
+    if (p1 > k) p1 = k;
+    float acc = 0.0f;
+    for (int64_t p = p0; p < p1; ++p) acc = ftz(fmaf(ae[p], be[p * ldb + j], acc));
+    int lvl = 0;
+    while (occ & (1ull << lvl)) {
+      acc = ftz(slot[lvl] + acc);
+      occ &= ~(1ull << lvl);
+      ++lvl;
+    }
+    slot[lvl] = acc;
+    occ |= 1ull << lvl;
+  }
+  float r = 0.0f;
+  int have = 0;
+  for (int lvl = 0; lvl < 48; ++lvl) {
+    if (!(occ & (1ull << lvl))) continue;
+    r = have ? ftz(slot[lvl] + r) : slot[lvl];
+    have = 1;
+  }
+  return ftz(r);
+}
+
+/* A_eff (m x k, flushed) and B_eff (k x n, flushed) are materialised once; then rows
+ * are spread over threads.  Output bits equal orc_gemm's. */
+void orc_gemm_fast(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k,
+                   int op, int64_t leaf, int nthreads) {
+  if (leaf <= 0) leaf = orc_leaf_size(k);
+  int64_t pc = orc_leaf_count(k, leaf);
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+  if (pc == 0) {
+    for (int64_t i = 0; i < m * n; ++i) c[i] = 0.0f;
+    return;
+  }
+  float* ae = (float*)malloc(sizeof(float) * (size_t)(m * k));
+  float* be = (float*)malloc(sizeof(float) * (size_t)(k * n));
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t p = 0; p < k; ++p) ae[i * k + p] = ftz(a_at(a, op, i, p, m, k));
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+  for (int64_t p = 0; p < k; ++p)
+    for (int64_t j = 0; j < n; ++j) be[p * n + j] = ftz(b_at(b, op, p, j, n, k));
+  const int64_t panel = 8 * FAST_VEC;
+  const int64_t npan = n / panel;
+  /* work items: (row, panel) pairs, so skinny-m shapes still spread over threads */
+  const int64_t items = m * (npan + 1);
+#pragma omp parallel for num_threads(nthreads) schedule(dynamic, 4)
+  for (int64_t it = 0; it < items; ++it) {
+    int64_t i = it / (npan + 1), pj = it % (npan + 1);
+    if (pj < npan) {
+      fast_panel(c + i * n, ae + i * k, be, n, pj * panel, k, leaf, pc);
+    } else {
+      for (int64_t j = npan * panel; j < n; ++j) c[i * n + j] = fast_cell(ae + i * k, be, n, j, k, leaf, pc);
+    }
+  }
+  free(ae);
+  free(be);
+}
+
+/* ---------------- seams around the product ---------------- */
+
+/* transformer/impl/llama/modeling_llama.mojo:3979-3989: y = ftz(ftz(y) + ftz(b[col])). */
+void orc_bias(float* y, const float* bias, int64_t m, int64_t n) {
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) y[i * n + j] = ftz(ftz(y[i * n + j]) + ftz(bias[j]));
+}
+
+/* core/nan_canon.mojo:55-110: every NaN word becomes 0x7FC00000, nothing else moves. */
+void orc_nan_canon(float* x, int64_t count) {
+  uint32_t* w = (uint32_t*)x;
+  for (int64_t i = 0; i < count; ++i)
+    if ((w[i] & 0x7FFFFFFFu) > 0x7F800000u) w[i] = 0x7FC00000u;
+}
+
+/* checks/numerics.mojo:1548-1551 (L-1): bits << 16, exact. */
+void orc_bf16_widen(float* out, const uint16_t* in, int64_t count) {
+  for (int64_t i = 0; i < count; ++i) out[i] = u2f((uint32_t)in[i] << 16);
+}
+
+/* checks/numerics.mojo:1554-1574 (L-2): ftz, then RNE on the low 16 bits; a NaN stays a
+ * quiet NaN with its sign and top payload bits; overflow rounds into the infinity. */
+void orc_bf16_narrow(uint16_t* out, const float* in, int64_t count) {
+  for (int64_t i = 0; i < count; ++i) {
+    uint32_t bb = f2u(ftz(in[i]));
+    if ((bb & 0x7F800000u) == 0x7F800000u && (bb & 0x007FFFFFu) != 0u) {
+      out[i] = (uint16_t)((bb >> 16) | 0x0040u);
+      continue;
+    }
+    uint32_t lsb = (bb >> 16) & 1u;
+    out[i] = (uint16_t)((bb + 0x7FFFu + lsb) >> 16);
+  }
+}
+
+/* The per-output-channel int8 weight of the decode workload: W_eff = ftz(f32(code) * ftz(scale[j])),
+ * one RNE multiply (the checks/numerics.mojo:1665-1671 spelling with the power of two replaced
+ * by an fp32 scale, flushed like every other operand seam).  `codes` is laid out as the B operand of `op` (k x n for NN/TN, n x k
+ * for NT); the output is the dequantised matrix in the same layout. */
+void orc_int8_dequant(float* out, const int8_t* codes, const float* scales, int64_t n, int64_t k,
+                      int op) {
+  for (int64_t p = 0; p < k; ++p)
+    for (int64_t j = 0; j < n; ++j) {
+      int64_t idx = op == OP_NT ? j * k + p : p * n + j;
+      out[idx] = ftz((float)codes[idx] * ftz(scales[j]));
+    }
+}
+
+/* core/identity_trace.mojo:89-115: FNV-1a64 over bytes in order. */
+uint64_t orc_fnv1a64(const void* data, int64_t nbytes) {
+  const uint8_t* p = (const uint8_t*)data;
+  uint64_t h = 0xCBF29CE484222325ull;
+  for (int64_t i = 0; i < nbytes; ++i) h = (h ^ (uint64_t)p[i]) * 0x100000001B3ull;
+  return h;
+}
+
+/* bench/gemm_card_main.mojo:292-311: a splitmix64-style mix of (index, salt), then
+ * <int in [-1048575, 1048575]> / 2^20, exact in binary32. */
+static inline uint64_t card_mix(int64_t i, int64_t salt) {
+  uint64_t z = (uint64_t)(i + 1) * 0x9E3779B97F4A7C15ull + (uint64_t)(salt + 1) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+void orc_card_fill(float* out, int64_t count, int64_t salt) {
+  for (int64_t i = 0; i < count; ++i) {
+    int64_t num = (int64_t)(card_mix(i, salt) % 2097151ull) - 1048575;
+    out[i] = (float)num / 1048576.0f;
+  }
+}
+
+int orc_max_threads(void) { return omp_get_max_threads(); }

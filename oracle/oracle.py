@@ -1,0 +1,179 @@
+"""ctypes wrapper of the CPU oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module, and only as the checker.  The product (mojolearn_amd) never calls it.
+
+Each function restates a reference function; the file:line is on the C side
+(oracle/gemm_oracle.c).
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+OP_NN, OP_NT, OP_TN = 0, 1, 2
+
+
+def build():
+    """Compile liboracle.so in place (gcc; see oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        i64, vp, c_int, f32 = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        L.orc_leaf_size.argtypes = [i64]; L.orc_leaf_size.restype = i64
+        L.orc_leaf_count.argtypes = [i64, i64]; L.orc_leaf_count.restype = i64
+        L.orc_gemm.argtypes = [vp, vp, vp, i64, i64, i64, c_int, i64]; L.orc_gemm.restype = None
+        L.orc_gemm_serial.argtypes = [vp, vp, vp, i64, i64, i64, c_int]; L.orc_gemm_serial.restype = None
+        L.orc_gemm_fast.argtypes = [vp, vp, vp, i64, i64, i64, c_int, i64, c_int]; L.orc_gemm_fast.restype = None
+        L.orc_fold_tree.argtypes = [vp, i64]; L.orc_fold_tree.restype = f32
+        L.orc_fold_stack.argtypes = [vp, i64]; L.orc_fold_stack.restype = f32
+        L.orc_bias.argtypes = [vp, vp, i64, i64]; L.orc_bias.restype = None
+        L.orc_nan_canon.argtypes = [vp, i64]; L.orc_nan_canon.restype = None
+        L.orc_bf16_widen.argtypes = [vp, vp, i64]; L.orc_bf16_widen.restype = None
+        L.orc_bf16_narrow.argtypes = [vp, vp, i64]; L.orc_bf16_narrow.restype = None
+        L.orc_int8_dequant.argtypes = [vp, vp, vp, i64, i64, c_int]; L.orc_int8_dequant.restype = None
+        L.orc_fnv1a64.argtypes = [vp, i64]; L.orc_fnv1a64.restype = ctypes.c_uint64
+        L.orc_card_fill.argtypes = [vp, i64, i64]; L.orc_card_fill.restype = None
+        L.orc_ftz.argtypes = [f32]; L.orc_ftz.restype = f32
+        L.orc_fma.argtypes = [f32, f32, f32]; L.orc_fma.restype = f32
+        L.orc_max_threads.argtypes = []; L.orc_max_threads.restype = c_int
+        _lib = L
+    return _lib
+
+
+def _p(x):
+    return x.ctypes.data_as(ctypes.c_void_p)
+
+
+def _shape(a, b, op):
+    if op == OP_NN:
+        (m, k), (kb, n) = a.shape, b.shape
+    elif op == OP_NT:
+        (m, k), (n, kb) = a.shape, b.shape
+    elif op == OP_TN:
+        (k, m), (kb, n) = a.shape, b.shape
+    else:
+        raise ValueError(op)
+    assert k == kb, (a.shape, b.shape, op)
+    return m, n, k
+
+
+def _f32c(x):
+    x = np.ascontiguousarray(x)
+    assert x.dtype == np.float32
+    return x
+
+
+def leaf_size(k):
+    return lib().orc_leaf_size(k)
+
+
+def leaf_count(k, leaf):
+    return lib().orc_leaf_count(k, leaf)
+
+
+def gemm(a, b, op=OP_NN, leaf=0):
+    """gemm/host/gemm_oracle.mojo:357-371 `gemm_oracle` (leaf=0), or `gemm_oracle_at_leaf`."""
+    a, b = _f32c(a), _f32c(b)
+    m, n, k = _shape(a, b, op)
+    c = np.empty((m, n), np.float32)
+    lib().orc_gemm(_p(c), _p(a), _p(b), m, n, k, op, leaf)
+    return c
+
+
+def gemm_serial(a, b, op=OP_NN):
+    """gemm/host/gemm_oracle.mojo:473-524 `gemm_oracle_serial`."""
+    a, b = _f32c(a), _f32c(b)
+    m, n, k = _shape(a, b, op)
+    c = np.empty((m, n), np.float32)
+    lib().orc_gemm_serial(_p(c), _p(a), _p(b), m, n, k, op)
+    return c
+
+
+def gemm_fast(a, b, op=OP_NN, leaf=0, threads=0):
+    """Same bits as `gemm`, AVX2 + threads (role of gemm/host/gemm_host_rows.mojo)."""
+    a, b = _f32c(a), _f32c(b)
+    m, n, k = _shape(a, b, op)
+    c = np.empty((m, n), np.float32)
+    lib().orc_gemm_fast(_p(c), _p(a), _p(b), m, n, k, op, leaf, threads)
+    return c
+
+
+def fold_tree(parts):
+    buf = np.array(parts, dtype=np.float32, copy=True)
+    return np.float32(lib().orc_fold_tree(_p(buf), len(buf)))
+
+
+def fold_stack(parts):
+    buf = np.ascontiguousarray(np.asarray(parts, dtype=np.float32))
+    return np.float32(lib().orc_fold_stack(_p(buf), len(buf)))
+
+
+def bias(y, b):
+    y = np.array(y, dtype=np.float32, copy=True)
+    b = _f32c(b)
+    lib().orc_bias(_p(y), _p(b), y.shape[0], y.shape[1])
+    return y
+
+
+def nan_canon(x):
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().orc_nan_canon(_p(x), x.size)
+    return x
+
+
+def bf16_widen(bits):
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().orc_bf16_widen(_p(out), _p(bits), bits.size)
+    return out
+
+
+def bf16_narrow(x):
+    x = _f32c(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_bf16_narrow(_p(out), _p(x), x.size)
+    return out
+
+
+def int8_dequant(codes, scales, op=OP_NN):
+    """W_eff = ftz(f32(code) * scale[col]) in the B layout of `op`."""
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    scales = _f32c(scales)
+    if op == OP_NT:
+        n, k = codes.shape
+    else:
+        k, n = codes.shape
+    out = np.empty(codes.shape, np.float32)
+    lib().orc_int8_dequant(_p(out), _p(codes), _p(scales), n, k, op)
+    return out
+
+
+def fnv1a64(x):
+    x = np.ascontiguousarray(x)
+    return int(lib().orc_fnv1a64(_p(x), x.nbytes))
+
+
+def card_fill(count, salt):
+    out = np.empty(count, np.float32)
+    lib().orc_card_fill(_p(out), count, salt)
+    return out
+
+
+def ftz(x):
+    return np.float32(lib().orc_ftz(float(np.float32(x))))
+
+
+def max_threads():
+    return lib().orc_max_threads()

@@ -1,0 +1,106 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every symbol
+include/mlgemm.h declares, the metadata ops of the op table answer, the error protocol,
+the Python surface's refusals (same texts and exception types as the reference door,
+bindings/linalg_ops_lowbit_door.mojo:259-416), and the workload generators."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from mojolearn_amd import _native, linalg
+from mojolearn_amd import workloads as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "mlgemm.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int64_t|int|const char\*)\s+(\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _native.lib()
+    names = _declared()
+    assert "linalg_native_v1" in names and "mlg_gemm_f32" in names
+    for name in names:
+        assert hasattr(L, name), name
+
+
+def test_metadata_ops():
+    assert _native.call(11, [], []) == 1
+    assert _native.call(12, [], []) == 1
+    assert _native.call(13, [], []) == 1
+    assert _native.call(14, [], []) == 1
+    assert _native.lib().mlg_abi_name() == b"mojolearn.linalg.v1"
+    assert linalg.numeric_mode() == "identical"
+    p = linalg.profile()
+    assert p["profile"] == "mojolearn.identical.gemm.fp32.v1" and p["identity_claimed"]
+
+
+def test_op_table_errors_come_through_the_sink_once():
+    with pytest.raises(RuntimeError, match="linalg native ABI: unknown operation"):
+        _native.call(99, [], [])
+    with pytest.raises(RuntimeError, match="metadata takes no descriptors"):
+        _native.call(11, [1], [])
+    with pytest.raises(RuntimeError, match="invalid gemm address count"):
+        _native.call(0, [1, 2], [1, 1, 1, 0])
+    with pytest.raises(RuntimeError, match=r"params must contain 4 values \(m, n, k, op\), got 3"):
+        _native.call(0, [1, 2, 3], [1, 1, 1])
+    with pytest.raises(RuntimeError, match="must all be positive"):
+        _native.call(0, [1, 2, 3], [0, 1, 1, 0])
+    with pytest.raises(RuntimeError, match="not part of this build"):
+        _native.call(2, [1, 2, 3, 4, 5], [1, 1, 1])
+    L = _native.lib()
+    msgs = []
+    sink = _native.SINK_T(lambda ctx, p, n: msgs.append((ctx, ctypes.string_at(p, n))))
+    r = ctypes.c_int64(0)
+    assert L.linalg_native_v1(12, 0, 0, 0, 0, 0, 1, ctypes.addressof(r), 77, sink) == 1
+    assert msgs == [(77, b"linalg native ABI: invalid result or scalar span")]
+
+
+def test_surface_refusals():
+    a = np.ones((4, 3), np.float32)
+    with pytest.raises(TypeError, match="only float32 is in this profile"):
+        linalg.matmul(a.astype(np.float64), a.T.copy())
+    with pytest.raises(ValueError, match="must be 2-D"):
+        linalg.matmul(np.ones(3, np.float32), a)
+    with pytest.raises(ValueError, match="no elements"):
+        linalg.matmul(np.ones((0, 3), np.float32), a)
+    with pytest.raises(ValueError, match="transpose_a=True with transpose_b=True is refused"):
+        linalg.matmul(a, a, transpose_a=True, transpose_b=True)
+    with pytest.raises(ValueError, match="contracted extents disagree"):
+        linalg.matmul(a, a)
+    with pytest.raises(TypeError, match="out has dtype float64"):
+        linalg.matmul(a, a.T.copy(), out=np.empty((4, 4)))
+    with pytest.raises(ValueError, match="out has shape"):
+        linalg.matmul(a, a.T.copy(), out=np.empty((4, 5), np.float32))
+    with pytest.raises(ValueError, match="must be C-contiguous"):
+        linalg.matmul(a, a.T.copy(), out=np.empty((4, 8), np.float32)[:, ::2])
+    ro = np.empty((4, 4), np.float32)
+    ro.flags.writeable = False
+    with pytest.raises(ValueError, match="read-only"):
+        linalg.matmul(a, a.T.copy(), out=ro)
+    with pytest.raises(TypeError, match="bf16 BITS in a uint16 buffer"):
+        linalg.matmul_bf16(a, a)
+    with pytest.raises(ValueError, match="is not one of the contract's three operations"):
+        linalg.matmul_bf16(a, np.ones((3, 4), np.uint16), transpose_a=True, transpose_b=True)
+
+
+def test_workload_bf16_narrow_matches_oracle(oracle):
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(200000) * np.exp2(rng.uniform(-140, 130, 200000))).astype(np.float32)
+    specials = np.array([0x7F800001, 0xFFC00001, 0x7F800000, 0x00000001, 0x80000001, 0x7F7FFFFF,
+                         0x3F808000, 0x3F818000, 0x00800000], np.uint32).view(np.float32)
+    x = np.concatenate([x, specials])
+    assert np.array_equal(W.bf16_narrow(x), oracle.bf16_narrow(x))
+
+
+def test_workload_generators_are_deterministic():
+    a, b = W.gemm512()
+    assert a.dtype == np.float32 and a.shape == (512, 512) and a.min() >= -1 and a.max() < 1
+    x16, codes, scales = W.decode()
+    assert codes.dtype == np.int8 and codes.min() >= -127 and scales.min() >= 1e-3 and scales.max() <= 1e-2
+    a2, _ = W.gemm512()
+    assert np.array_equal(a, a2)

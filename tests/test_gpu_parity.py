@@ -1,0 +1,200 @@
+"""Parity of the gfx950 kernels (through the C ABI) with the reference, bit for bit.
+
+* the MI325X device card's 20 full-shape rows (hashes recorded by the reference's own device
+  kernel, byte-identical to its NVIDIA card) and the host-capped oracle card;
+* closed-form fixtures F1-F8, inf/NaN (tests/kat.py);
+* the CPU oracle on random shapes: ragged m/n/k, every orientation, wide exponents,
+  subnormals, signed zeros, inf/NaN; bf16 and int8 weights; the fused bias; caller leaves;
+* the five workloads at their real sizes on row samples (cells are independent of m, so a
+  row subset through the oracle is the same bits as the whole product's rows).
+"""
+import numpy as np
+import pytest
+
+import cards
+import kat
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _dev():
+    from mojolearn_amd import device
+    return device
+
+
+def gpu_gemm(a, b, op, leaf=0, bias=None):
+    D = _dev()
+    ta = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    tb = torch.from_numpy(np.ascontiguousarray(b)).to(DEV)
+    tbias = None if bias is None else torch.from_numpy(np.ascontiguousarray(bias)).to(DEV)
+    c = D.gemm(ta, tb, op=op, leaf=leaf, bias=tbias)
+    torch.cuda.synchronize()
+    return c.cpu().numpy()
+
+
+def words(x):
+    return np.ascontiguousarray(x).view(np.uint32)
+
+
+def assert_bits(got, want, what=""):
+    g, w = words(got), words(want)
+    bad = np.flatnonzero(g.ravel() != w.ravel())
+    if bad.size:
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {g.size} words differ; first at flat {i}: "
+                             f"got {g.ravel()[i]:#010x} want {w.ravel()[i]:#010x}")
+
+
+def _card_inputs(O, i, m, n, k, op):
+    sa, sb = cards.operand_shapes(m, n, k, op)
+    return O.card_fill(m * k, 11 + i).reshape(sa), O.card_fill(n * k, 22 + i).reshape(sb)
+
+
+DEVICE_CARD = cards.parse_card("device_mi325x.card")
+HOST_CARD = cards.parse_card("host_oracle.card")
+
+
+@pytest.mark.parametrize("row", cards.device_rows(), ids=[r[1] for r in cards.device_rows()])
+def test_device_card_full_shape(oracle, row):
+    """Output hash of the reference's own device run (MI325X card) at the full card shape."""
+    i, name, m, n, k, op = row
+    print(f"device card {name}: m={m} n={n} k={k} op={op}", flush=True)
+    a, b = _card_inputs(oracle, i, m, n, k, op)
+    c = gpu_gemm(a, b, op)
+    assert (c.size, oracle.fnv1a64(c)) == DEVICE_CARD[name + ".out"], name
+
+
+@pytest.mark.parametrize("i", range(len(cards.SHAPES)), ids=[s[0] for s in cards.SHAPES])
+def test_host_card_capped_shape(oracle, i):
+    name, m0, n0, k, op = cards.SHAPES[i]
+    m, n = cards.host_capped(m0, n0, k)
+    a, b = _card_inputs(oracle, i, m, n, k, op)
+    c = gpu_gemm(a, b, op)
+    assert (c.size, oracle.fnv1a64(c)) == HOST_CARD[name + ".out"], name
+
+
+@pytest.mark.parametrize("fx", kat.fixtures(), ids=[f[0] for f in kat.fixtures()])
+def test_kat_gpu(fx):
+    name, a, b, leaf, want = fx
+    c = gpu_gemm(a.reshape(1, -1), b.reshape(1, -1), 1, leaf=leaf)
+    assert words(c)[0, 0] == want, (name, hex(int(words(c)[0, 0])), hex(int(want)))
+
+
+def _values(rng, shape, kind):
+    if kind == "normal":
+        return rng.standard_normal(shape).astype(np.float32)
+    if kind == "wide":  # exponents over most of the range, subnormals, signed zeros
+        x = (rng.standard_normal(shape) * np.exp2(rng.uniform(-140, 60, shape))).astype(np.float32)
+        z = rng.random(shape)
+        x[z < 0.02] = np.float32(0.0)
+        x[(z >= 0.02) & (z < 0.04)] = np.float32(-0.0)
+        return x
+    if kind == "special":  # + a few inf/NaN
+        x = _values(rng, shape, "wide")
+        z = rng.random(shape)
+        x[z < 0.001] = np.float32(np.inf)
+        x[(z >= 0.001) & (z < 0.002)] = np.float32(-np.inf)
+        x[(z >= 0.002) & (z < 0.0025)] = np.float32(np.nan)
+        return x
+    raise ValueError(kind)
+
+
+def _operands(rng, m, n, k, op, kind):
+    A = _values(rng, (m, k), kind)
+    B = _values(rng, (k, n), kind)
+    a = A if op != 2 else np.ascontiguousarray(A.T)
+    b = B if op != 1 else np.ascontiguousarray(B.T)
+    return a, b
+
+
+SHAPES = [(1, 1, 1), (5, 7, 3), (17, 33, 129), (130, 129, 300), (128, 128, 128), (257, 255, 517),
+          (64, 300, 1024), (3, 1000, 4097), (200, 64, 2048), (4, 5, 100003), (2, 3, 131073), (96, 97, 14336)]
+
+
+@pytest.mark.parametrize("kind", ["normal", "wide", "special"])
+@pytest.mark.parametrize("op", [0, 1, 2])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in SHAPES])
+def test_random_vs_oracle(oracle, shape, op, kind):
+    m, n, k = shape
+    rng = np.random.default_rng(m * 7 + n * 13 + k * 17 + op)
+    a, b = _operands(rng, m, n, k, op, kind)
+    print(f"random {kind} op={op} m={m} n={n} k={k}", flush=True)
+    want = oracle.nan_canon(oracle.gemm_fast(a, b, op))
+    assert_bits(gpu_gemm(a, b, op), want, f"{shape} op={op} {kind}")
+
+
+@pytest.mark.parametrize("leaf", [1, 7, 64, 300, 1000])
+def test_caller_leaf(oracle, leaf):
+    """A caller-given partition (the sequence-executor word is leaf = k, one chain)."""
+    rng = np.random.default_rng(leaf)
+    m, n, k = 33, 65, 1000
+    a, b = _operands(rng, m, n, k, 0, "wide")
+    assert_bits(gpu_gemm(a, b, 0, leaf=leaf), oracle.gemm_fast(a, b, 0, leaf=leaf), f"leaf={leaf}")
+    serial = gpu_gemm(a, b, 0, leaf=k)
+    assert_bits(serial, oracle.gemm_serial(a, b, 0), "serial word")
+
+
+def test_k_zero_writes_plus_zero():
+    D = _dev()
+    a = torch.empty((3, 0), dtype=torch.float32, device=DEV)
+    b = torch.empty((0, 5), dtype=torch.float32, device=DEV)
+    c = torch.full((3, 5), -987654.0, device=DEV)
+    D.gemm(a, b, op=0, out=c)
+    torch.cuda.synchronize()
+    assert np.all(words(c.cpu().numpy()) == 0)
+
+
+@pytest.mark.parametrize("op", [0, 1])
+def test_bias_epilogue(oracle, op):
+    rng = np.random.default_rng(11 + op)
+    m, n, k = 70, 150, 640
+    a, b = _operands(rng, m, n, k, op, "wide")
+    bias = _values(rng, (n,), "wide")
+    want = oracle.nan_canon(oracle.bias(oracle.gemm_fast(a, b, op), bias))
+    assert_bits(gpu_gemm(a, b, op, bias=bias), want, "bias")
+
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+@pytest.mark.parametrize("a_bits", [False, True])
+def test_bf16_weights(oracle, op, a_bits):
+    D = _dev()
+    rng = np.random.default_rng(21 + op)
+    m, n, k = 67, 131, 777
+    a, b = _operands(rng, m, n, k, op, "wide")
+    bb = oracle.bf16_narrow(b)
+    aa = oracle.bf16_narrow(a) if a_bits else a
+    want = oracle.nan_canon(oracle.gemm_fast(oracle.bf16_widen(aa) if a_bits else aa, oracle.bf16_widen(bb), op))
+    ta = torch.from_numpy(aa.view(np.int16) if a_bits else aa).to(DEV)
+    c = D.gemm_bf16w(ta, torch.from_numpy(bb.view(np.int16)).to(DEV), op=op)
+    torch.cuda.synchronize()
+    assert_bits(c.cpu().numpy(), want, "bf16")
+
+
+@pytest.mark.parametrize("op", [0, 1])
+@pytest.mark.parametrize("m", [1, 4, 16, 100])
+def test_int8_weights(oracle, op, m):
+    D = _dev()
+    rng = np.random.default_rng(31 + op + m)
+    n, k = 300, 1100
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    codes = rng.integers(-127, 128, (k, n) if op == 0 else (n, k), dtype=np.int8)
+    scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    want = oracle.nan_canon(oracle.gemm_fast(a, oracle.int8_dequant(codes, scales, op), op))
+    c = D.gemm_int8w(torch.from_numpy(a).to(DEV), torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV),
+                     op=op)
+    torch.cuda.synchronize()
+    assert_bits(c.cpu().numpy(), want, "int8")
+
+
+def test_bf16_conversions(oracle):
+    D = _dev()
+    bits = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    w = D.bf16_widen(torch.from_numpy(bits.view(np.int16)).to(DEV)).cpu().numpy()
+    assert_bits(w, oracle.bf16_widen(bits), "widen")
+    rng = np.random.default_rng(5)
+    x = _values(rng, (100000,), "special")
+    n = D.bf16_narrow(torch.from_numpy(x).to(DEV)).cpu().numpy().view(np.uint16)
+    assert np.array_equal(n, oracle.bf16_narrow(x))

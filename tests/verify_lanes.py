@@ -1,0 +1,134 @@
+"""The verify-table fixtures and gemm lanes, restated for the tests.
+
+Fixtures: tools/identity_break.py:1393 (N, D = 20000, 16) and :1414-1485 (`fixture`,
+`_hashed_uniform`).  Hashes: `_h` / `_train_hash` (:1355-1382).  Lanes: gemm-pinned
+(:2984-2995), gemm-transposed (:5880-5890), gemm-bf16 (:3825-3836).  The recorded
+`train` hashes are in tests/golden/verify_gemm_cells.json (from
+python/mojolearn/verify_reference/table.json).
+
+Each lane takes the three callables it needs, so the same lane runs against the CPU
+oracle (tests/test_oracle_golden.py) and against the MI355X surface
+(tests/test_gpu_surface.py).
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+
+N, D = 20000, 16
+FIXTURES = ["base", "ties", "hashed", "wide", "denormal", "denormal_ftz", "dupes", "odd", "negative"]
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "verify_gemm_cells.json")
+
+
+def golden():
+    with open(GOLDEN) as fh:
+        return json.load(fh)
+
+
+def h(*arrays):
+    m = hashlib.sha256()
+    for a in arrays:
+        a = np.ascontiguousarray(np.asarray(a))
+        m.update(str(a.dtype).encode())
+        m.update(str(a.shape).encode())
+        m.update(a.tobytes())
+    return m.hexdigest()[:16]
+
+
+def train_hash(parts):
+    return h(np.frombuffer("|".join(f"{k}={v}" for k, v in sorted(parts.items())).encode(), dtype=np.uint8))
+
+
+def _hashed_uniform(n, d, seed):
+    ctr = np.arange(n * d, dtype=np.uint64)
+    dig = hashlib.sha256(ctr.tobytes() + str(seed).encode()).digest()
+    stream = bytearray()
+    blk = 0
+    while len(stream) < n * d * 4:
+        stream += hashlib.sha256(dig + blk.to_bytes(8, "little")).digest()
+        blk += 1
+    u32 = np.frombuffer(bytes(stream[: n * d * 4]), dtype=np.uint32)
+    return (u32.astype(np.float64) / 2**32).astype(np.float32).reshape(n, d)
+
+
+def fixture_x(kind, n=N, d=D, seed=0):
+    rng = np.random.default_rng(seed)
+    if kind == "base":
+        X = rng.standard_normal((n, d)).astype(np.float32)
+    elif kind == "ties":
+        X = rng.integers(0, 6, size=(n, d)).astype(np.float32)
+    elif kind == "hashed":
+        X = (_hashed_uniform(n, d, seed) * 4.0 - 2.0).astype(np.float32)
+    elif kind == "wide":
+        X = rng.standard_normal((n, d)).astype(np.float32)
+        scale = np.logspace(-4, 4, d).astype(np.float32)
+        X = (X * scale).astype(np.float32)
+    elif kind == "denormal":
+        X = rng.standard_normal((n, d)).astype(np.float32)
+        X[: n // 4, :3] = (X[: n // 4, :3] * np.float32(1e-40)).astype(np.float32)
+    elif kind == "denormal_ftz":
+        X = fixture_x("denormal", n, d, seed)
+        sub = (X != 0) & (np.abs(X) < np.finfo(np.float32).tiny)
+        X = X.copy()
+        X[sub] = np.copysign(np.float32(0.0), X[sub])
+    elif kind == "dupes":
+        X = rng.standard_normal((n, d)).astype(np.float32)
+        X[n // 2:] = X[: n - n // 2]
+        X[:, d - 2] = np.float32(3.5)
+        X[:, d - 1] = np.float32(0.0)
+    elif kind == "odd":
+        n, d = 12345, 17
+        X = rng.standard_normal((n, d)).astype(np.float32)
+    elif kind == "negative":
+        X = (-np.abs(rng.standard_normal((n, d))) - 2.0).astype(np.float32)
+    else:
+        raise ValueError(kind)
+    return X
+
+
+def lane_gemm_pinned(matmul, X):
+    a = X[:256].T.copy()
+    c1 = np.asarray(matmul(a.astype(np.float32), X[:256].astype(np.float32)))
+    # X.size < 256 * 4096 for every fixture, so the lane's `wide` product is c1 again
+    assert X.size < 256 * 4096
+    return dict(small=h(c1), wide=h(c1))
+
+
+def lane_gemm_transposed(matmul, X):
+    a = np.ascontiguousarray(X[:256]).astype(np.float32)
+    b = np.ascontiguousarray(X[256:384]).astype(np.float32)
+    nt = np.asarray(matmul(a, b, transpose_b=True))
+    at = np.ascontiguousarray(X[:256].T).astype(np.float32)
+    c = np.ascontiguousarray(X[384:384 + at.shape[0]]).astype(np.float32)
+    tn = np.asarray(matmul(at, c, transpose_a=True))
+    return dict(nt=h(nt), tn=h(tn))
+
+
+def lane_gemm_bf16(to_bf16, matmul_bf16, X):
+    a = np.ascontiguousarray(X[:256]).astype(np.float32)
+    b = np.ascontiguousarray(X[256:256 + 128]).astype(np.float32)
+    bb = np.asarray(to_bf16(b))
+    c1 = np.asarray(matmul_bf16(a, bb, transpose_b=True))
+    c2 = np.asarray(matmul_bf16(np.asarray(to_bf16(a)), bb, transpose_b=True))
+    c3 = np.asarray(matmul_bf16(np.ascontiguousarray(a[:64].T), np.asarray(to_bf16(a[64:128]))))
+    return dict(nt=h(c1), both=h(c2), nn=h(c3), bits=h(bb))
+
+
+class OracleSurface:
+    """The three surface calls the lanes need, answered by the CPU oracle."""
+
+    def __init__(self, O):
+        self.O = O
+
+    def matmul(self, a, b, transpose_a=False, transpose_b=False, identical=True):
+        op = 2 if transpose_a else (1 if transpose_b else 0)
+        return self.O.nan_canon(self.O.gemm(a, b, op))
+
+    def to_bf16(self, x):
+        return self.O.bf16_narrow(np.ascontiguousarray(x, dtype=np.float32))
+
+    def matmul_bf16(self, a, b, transpose_a=False, transpose_b=False):
+        a = np.asarray(a)
+        af = self.O.bf16_widen(a) if a.dtype == np.uint16 else a
+        return self.matmul(af, self.O.bf16_widen(b), transpose_a, transpose_b)
