@@ -25,17 +25,25 @@ FP32_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
 HBM_PEAK_GBS = 8000.0
 
 
-def _events_time(fn, steps, warmup, torch):
-    """Average ms per call of `fn` over `steps` timed calls on the current stream."""
-    for _ in range(warmup):
-        fn()
+def graph_time(calls, steps, warmup, torch):
+    """Average ms per call: `steps` calls (round-robin over `calls`, each a Plan) captured in one
+    HIP graph on a private stream and replayed; HIP events on the replaying stream."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for i in range(max(warmup, len(calls))):
+            calls[i % len(calls)](s)
     torch.cuda.synchronize()
-    s = torch.cuda.current_stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(steps):
+            calls[i % len(calls)](s)
+    g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for _ in range(steps):
-        fn()
-    e1.record(s)
+    e0.record(cur)
+    g.replay()
+    e1.record(cur)
     e1.synchronize()
     return e0.elapsed_time(e1) / steps
 
@@ -48,93 +56,83 @@ def _mismatch(got, want):
     return int(np.count_nonzero(np.ascontiguousarray(got).view(np.uint32) != np.ascontiguousarray(want).view(np.uint32)))
 
 
+def _t(torch, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+
+
 def bench_prefill(torch, D, W, O, steps, warmup, check):
     x, w, bias = W.prefill()
-    dev = "cuda:0"
-    tx, tw, tb = (torch.from_numpy(v).to(dev) for v in (x, w, bias))
-    out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=dev)
-    fn = lambda: D.gemm(tx, tw, bias=tb, out=out)  # noqa: E731
-    ms = _events_time(fn, steps, warmup, torch)
+    plan = D.Plan(_t(torch, x), _t(torch, w), bias=_t(torch, bias))
+    ms = graph_time([plan], steps, warmup, torch)
     m, k = x.shape
     n = w.shape[1]
     res = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
     if check:
         rows = _rows(m)
         want = O.nan_canon(O.bias(O.gemm_fast(x[rows], w, 0), bias))
-        res["mismatched_words"] = _mismatch(out.cpu().numpy()[rows], want)
+        res["mismatched_words"] = _mismatch(plan.out.cpu().numpy()[rows], want)
         res["checked_cells"] = int(rows.size * n)
     return res
 
 
-def bench_gemm_generic(torch, D, a, b, steps, warmup, kind="f32", O=None, check_rows=None, want_fn=None):
-    dev = "cuda:0"
-    ta = torch.from_numpy(a).to(dev)
-    if kind == "bf16":
-        tb = torch.from_numpy(b.view(np.int16)).to(dev)
-        fn = lambda: D.gemm_bf16w(ta, tb, out=out)  # noqa: E731
-    else:
-        tb = torch.from_numpy(b).to(dev)
-        fn = lambda: D.gemm(ta, tb, out=out)  # noqa: E731
+def bench_product(torch, D, a, b, steps, warmup, want_fn=None):
+    """One Plan (a: float32, b: float32 or bf16 bits as uint16) timed as graph replays."""
+    tb = _t(torch, b.view(np.int16) if b.dtype == np.uint16 else b)
+    plan = D.Plan(_t(torch, a), tb)
+    ms = graph_time([plan], steps, warmup, torch)
     m, k = a.shape
     n = b.shape[1]
-    out = torch.empty((m, n), dtype=torch.float32, device=dev)
-    ms = _events_time(fn, steps, warmup, torch)
     res = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
     if want_fn is not None:
-        rows = check_rows if check_rows is not None else _rows(m)
-        res["mismatched_words"] = _mismatch(out.cpu().numpy()[rows], want_fn(rows))
+        rows = _rows(m)
+        res["mismatched_words"] = _mismatch(plan.out.cpu().numpy()[rows], want_fn(rows))
         res["checked_cells"] = int(len(rows) * n)
     return res
 
 
 def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8):
-    """int8-weight GEMV; `nbuf` distinct weight buffers (> 256 MB Infinity Cache) rotate so W
-    comes from HBM.  GB/s counts K*N int8 codes + N scales + M*K x + M*N y."""
+    """int8-weight GEMV; `nbuf` distinct weight buffers (8 x 58.7 MB > the 256 MB Infinity
+    Cache) rotate so W streams from HBM.  GB/s counts K*N int8 codes + N scales + M*K x +
+    M*N y per call."""
     x16, codes, scales = W.decode()
     x = np.ascontiguousarray(x16[:m])
-    dev = "cuda:0"
-    tx = torch.from_numpy(x).to(dev)
-    tcodes = [torch.from_numpy(codes).to(dev)] + [torch.from_numpy(np.roll(codes, i, axis=1)).to(dev)
-                                                  for i in range(1, nbuf)]
-    ts = torch.from_numpy(scales).to(dev)
+    tx, ts = _t(torch, x), _t(torch, scales)
+    out = torch.empty((m, codes.shape[1]), dtype=torch.float32, device="cuda:0")
+    tcodes = [_t(torch, codes)] + [_t(torch, np.roll(codes, i, axis=1)) for i in range(1, nbuf)]
+    plans = [D.Plan(tx, tc, scales=ts, out=out) for tc in tcodes]
+    ms = graph_time(plans, max(steps, 2 * nbuf), warmup, torch)
     k, n = codes.shape
-    out = torch.empty((m, n), dtype=torch.float32, device=dev)
-    it = [0]
-
-    def fn():
-        D.gemm_int8w(tx, tcodes[it[0] % nbuf], ts, out=out)
-        it[0] += 1
-
-    ms = _events_time(fn, max(steps, nbuf), warmup, torch)
     nbytes = k * n + 4 * n + 4 * m * k + 4 * m * n
-    res = {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
-           "bytes": nbytes}
+    res = {"ms": ms, "us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
+           "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "bytes": nbytes}
     if check:
-        D.gemm_int8w(tx, tcodes[0], ts, out=out)
+        plans[0]()
         want = O.gemm_fast(x, O.int8_dequant(codes, scales, 0), 0)
         res["mismatched_words"] = _mismatch(out.cpu().numpy(), want)
         res["checked_cells"] = int(m * n)
     return res
 
 
-def cpu_baseline(W, O, seconds=10.0):
-    """The CPU oracle's fast arm (AVX2 FMA, all host threads) on the prefill workload's first
-    rows, grown until the run takes about `seconds`; GFLOP/s of the same arithmetic."""
+def cpu_baseline(W, O, min_seconds=10.0, max_seconds=30.0):
+    """The CPU oracle's fast arm (AVX2 FMA, every host thread) on the whole prefill product,
+    repeated until about `min_seconds` have passed; GFLOP/s of the same arithmetic."""
     x, w, bias = W.prefill()
     threads = O.max_threads()
-    rows = 4
+    reps, t0 = 0, time.perf_counter()
     while True:
-        t0 = time.perf_counter()
-        y = O.gemm_fast(x[:rows], w, 0, threads=threads)
+        y = O.gemm_fast(x, w, 0, threads=threads)
         O.bias(y, bias)
+        reps += 1
         dt = time.perf_counter() - t0
-        if dt * 2 > seconds or rows >= 512:
+        if dt >= min_seconds or dt * (reps + 1) / reps > max_seconds:
             break
-        rows *= 2
-    n, k = w.shape[1], w.shape[0]
-    return {"value": 2.0 * rows * n * k / dt / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"prefill rows 0..{rows - 1} of 2048 (X[{rows}x4096] . W[4096x4096] + bias), "
-                      f"oracle/gemm_oracle.c fast arm, {threads} threads, {dt:.2f} s"}
+    m, k = x.shape
+    n = w.shape[1]
+    return {"value": round(2.0 * m * n * k * reps / dt / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"the whole prefill product (X[2048x4096] . W[4096x4096] + bias) x {reps}, "
+                      f"oracle/gemm_oracle.c fast arm (AVX2 FMA), {threads} threads, {dt:.1f} s"}
 
 
 def main():
@@ -163,16 +161,16 @@ def main():
     extra = {}
     if args.all:
         a, b = W.gemm512()
-        extra["gemm512"] = bench_gemm_generic(torch, D, a, b, args.steps, args.warmup,
-                                              want_fn=(lambda r: O.gemm(a[r], b, 0)) if check else None)
+        extra["gemm512"] = bench_product(torch, D, a, b, args.steps, args.warmup,
+                                         want_fn=(lambda r: O.gemm(a[r], b, 0)) if check else None)
         for m in (1, 4, 16):
             extra[f"decode_m{m}"] = bench_decode(torch, D, W, O, m, args.steps, args.warmup, check)
         x, wb = W.swiglu_up()
-        extra["swiglu_up"] = bench_gemm_generic(
-            torch, D, x, wb, max(3, args.steps // 4), 1, kind="bf16",
+        extra["swiglu_up"] = bench_product(
+            torch, D, x, wb, max(3, args.steps // 4), 1,
             want_fn=(lambda r: O.gemm_fast(x[r], O.bf16_widen(wb), 0)) if check else None)
         x, w = W.lm_head()
-        extra["lm_head"] = bench_gemm_generic(
+        extra["lm_head"] = bench_product(
             torch, D, x, w, max(3, args.steps // 2), 1,
             want_fn=(lambda r: O.nan_canon(O.gemm_fast(x[r], w, 0))) if check else None)
 

@@ -80,6 +80,21 @@ int mlg_gemm_int8w(float* c, const float* a, const int8_t* codes, const float* s
                    const float* bias, int64_t m, int64_t n, int64_t k, int32_t op, int64_t leaf,
                    void* stream);
 
+/* The general device entry with a caller-supplied workspace: it allocates no device memory
+ * for the product (so a caller may capture it in a HIP graph), apart from a per-(device,
+ * stream) buffer of completion counters created zeroed on the first call on that stream.
+ * a_type: 0 float32, 1 bf16 bits; b_type: 0 float32, 1 bf16 bits, 2 int8 codes (with
+ * `scales`, one per output column).  `workspace` must hold mlg_gemm_workspace_bytes() bytes
+ * (0 bytes for most shapes; NULL is then accepted).  Calls sharing one workspace must be
+ * ordered (one stream).  Same semantics as mlg_gemm_f32/bf16w/int8w otherwise. */
+int mlg_gemm_ws(float* c, const void* a, const void* b, const float* scales, const float* bias,
+                int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type,
+                int64_t leaf, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace mlg_gemm_ws needs for this product on the current device (-1 on error). */
+int64_t mlg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type,
+                                 int32_t b_type, int64_t leaf);
+
 /* L-1 / L-2 conversions on device buffers (checks/numerics.mojo:1548-1574). */
 int mlg_bf16_widen(float* out, const uint16_t* in, int64_t count, void* stream);
 int mlg_bf16_narrow(uint16_t* out, const float* in, int64_t count, void* stream);

@@ -39,6 +39,10 @@ def lib():
         L.mlg_gemm_bf16w.restype = ctypes.c_int
         L.mlg_gemm_int8w.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, i64, vp]
         L.mlg_gemm_int8w.restype = ctypes.c_int
+        L.mlg_gemm_ws.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i32, i64, vp, i64, vp]
+        L.mlg_gemm_ws.restype = ctypes.c_int
+        L.mlg_gemm_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i32, i64]
+        L.mlg_gemm_workspace_bytes.restype = i64
         L.mlg_bf16_widen.argtypes = [vp, vp, i64, vp]
         L.mlg_bf16_widen.restype = ctypes.c_int
         L.mlg_bf16_narrow.argtypes = [vp, vp, i64, vp]

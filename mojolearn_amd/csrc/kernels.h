@@ -21,9 +21,14 @@ struct GemmProblem {
 // Workspace floats run_gemm needs for `p` (0 when the product folds in one launch).
 int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus);
 
-// Enqueue the product on `stream`.  `ws` must hold gemm_workspace_floats() floats.
-// Returns hipSuccess or the launch error.
-hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t stream);
+// Completion counters the product needs (0 or one per 256-column block of the skinny-M
+// path); they must be zero on entry and are zero again when the product completes.
+int64_t gemm_counter_count(const GemmProblem& p);
+
+// Enqueue the product on `stream`.  `ws` must hold gemm_workspace_floats() floats and
+// `counters` gemm_counter_count() zeroed counters.  Returns hipSuccess or the launch error.
+hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int num_cus,
+                    hipStream_t stream);
 
 // Elementwise conversions used by the low-bit surface (to_bf16 / from_bf16).
 hipError_t run_bf16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream);

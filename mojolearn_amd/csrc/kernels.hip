@@ -31,6 +31,7 @@ namespace mlg {
 
 typedef float v32f __attribute__((ext_vector_type(32)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));  // 16 raw bytes
 
 // hwreg(HW_REG_MODE, 4, 2): FP_DENORM single-precision field.
 #define MLG_HWREG_FP_DENORM32 ((1 << 11) | (4 << 6) | 1)
@@ -455,7 +456,261 @@ __global__ void __launch_bounds__(256) fold_groups_kernel(float* c, const float*
 }
 
 // ---------------------------------------------------------------------------
+// Skinny-M product (decode GEMV), OP_NN: X[M x K] . W[K x N], M <= 16.
+//
+// Work is split into tasks: (block of 256 output columns, one k-leaf).  A persistent grid of
+// 256-thread workgroups walks its tasks leaf chunk by leaf chunk through one continuous
+// pipeline: the 256 threads stream the next chunk of W (R rows x 256 columns, 16-byte loads,
+// 32 KB) and of x into registers while the current chunk's chains run out of LDS, so HBM sees
+// a steady stream regardless of how the serial chains are owned.  Thread c runs the chain of
+// column c: a VALU FMA per step under MODE.FP_DENORM = 2 (v_fma_f32 is fma(ftz a, ftz b,
+// ftz acc), like the K=1 MFMA), for all M rows.  A finished leaf partial is published with
+// agent-scope atomic stores (device coherent, so no cache writeback is needed: the stores only
+// have to be complete before the count), counted on its column block's counter, and the task
+// that completes a block folds its P partials with the contract's tree, writes the output and
+// resets the counter.  One launch computes the whole product.
+constexpr int GV_THREADS = 256;
+constexpr int GV_COLS = 256;                // columns per task: one per thread
+constexpr int GV_MAXM = 16;
+constexpr int GV_CHUNK = 32768;             // bytes of W per LDS buffer
+constexpr int GV_FOLD_BATCH = 32;           // partial loads in flight while folding
+
+template <int T>
+struct GvElem {
+  static constexpr int bytes = T == T_F32 ? 4 : (T == T_BF16 ? 2 : 1);
+  static constexpr int rows = GV_CHUNK / (GV_COLS * bytes);  // rows per chunk: 128 / 64 / 32
+};
+
+struct GemvArgs {
+  float* c;
+  const float* x;
+  const void* w;
+  const float* scales;
+  const float* bias;
+  float* ws;              // [nleaves][m][n] leaf partials when nleaves > 1
+  unsigned int* counter;  // [column blocks], zero between launches
+  int64_t m, n, k, leaf, nleaves;
+  int64_t ncb;            // column blocks
+  int64_t ntasks;         // ncb * nleaves
+  int chunks;             // chunks per leaf: ceil(leaf / rows)
+};
+
+// Issue every global read of one chunk into registers; `store` writes them to LDS.  A
+// segment no chain step reads (a row outside the leaf, columns past n) is read from the
+// operand's first bytes instead -- an in-bounds address -- so the loads carry no branch and
+// are all in flight together; those LDS bytes only reach cells that are never stored.
+template <int T, int MR, bool VEC>
+struct GvStager {
+  static constexpr int EB = GvElem<T>::bytes;
+  static constexpr int R = GvElem<T>::rows;
+  static constexpr int SEGS = GV_COLS * EB / 16;           // 16-byte segments per row
+  static constexpr int PER = R * SEGS / GV_THREADS;        // segments per thread: 8
+  static constexpr int XPER = (R * MR + GV_THREADS - 1) / GV_THREADS;
+  u4 wv[PER];
+  float xv[XPER];
+
+  __device__ __forceinline__ void load(const GemvArgs& g, int64_t j0, int64_t t, int ch, int tid) {
+    const char* wb = static_cast<const char*>(g.w);
+    const int64_t kb = t * g.leaf + (int64_t)ch * R;
+    int64_t kend = (t + 1) * g.leaf;
+    if (kend > g.k) kend = g.k;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int q = tid + i * GV_THREADS;
+      const int rr = q / SEGS;
+      const int sg = q % SEGS;
+      const int64_t kk = kb + rr;
+      const int64_t col = j0 + (int64_t)sg * (16 / EB);
+      if constexpr (VEC) {
+        const bool ok = kk < kend && col < g.n;
+        wv[i] = *reinterpret_cast<const u4*>(ok ? wb + (kk * g.n + col) * EB : wb);
+      } else {
+        u4 v = {0u, 0u, 0u, 0u};
+        if (kk < kend) {
+          const char* src = wb + (kk * g.n + col) * EB;
+          char* d = reinterpret_cast<char*>(&v);
+#pragma unroll
+          for (int e = 0; e < 16 / EB; ++e)
+            if (col + e < g.n) {
+              if constexpr (EB == 4) reinterpret_cast<float*>(d)[e] = reinterpret_cast<const float*>(src)[e];
+              else if constexpr (EB == 2) reinterpret_cast<uint16_t*>(d)[e] = reinterpret_cast<const uint16_t*>(src)[e];
+              else d[e] = src[e];
+            }
+        }
+        wv[i] = v;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+      const int q = tid + i * GV_THREADS;
+      const int rr = q / MR;
+      const int r = q % MR;
+      const int64_t kk = kb + rr;
+      const bool ok = q < R * MR && kk < kend && r < g.m;
+      xv[i] = *(ok ? g.x + r * g.k + kk : g.x);  // rows past m feed cells that are never stored
+    }
+  }
+
+  __device__ __forceinline__ void store(char* buf, float* xbuf, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int q = tid + i * GV_THREADS;
+      *reinterpret_cast<u4*>(buf + (q / SEGS) * GV_COLS * EB + (q % SEGS) * 16) = wv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+      const int q = tid + i * GV_THREADS;
+      if (q < R * MR) xbuf[q] = xv[i];
+    }
+  }
+};
+
+// The contract's tree over a cell's P leaf partials ws[t * stride], read with agent-scope
+// atomic loads issued GV_FOLD_BATCH at a time.
+__device__ __forceinline__ float fold_partials(const float* base, int64_t P, int64_t stride) {
+  StackF stk;
+  int64_t t = 0;
+  float last = 0.f;
+  for (int64_t t0 = 0; t0 < P; t0 += GV_FOLD_BATCH) {
+    float v[GV_FOLD_BATCH];
+#pragma unroll
+    for (int e = 0; e < GV_FOLD_BATCH; ++e) {
+      const int64_t tt = t0 + e < P ? t0 + e : P - 1;
+      v[e] = __hip_atomic_load(base + tt * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int e = 0; e < GV_FOLD_BATCH; ++e) {
+      if (t0 + e >= P) break;
+      t = t0 + e;
+      if (t + 1 < P) stk.push(v[e], (int)t);
+      else last = v[e];
+    }
+  }
+  return stk.root(last, (int)t);
+}
+
+// The task that completed column block `cb`: fold each cell's P partials, write the output,
+// reset the block's counter.
+template <int MR>
+__device__ __forceinline__ void gv_finish(const GemvArgs& g, int64_t cb, int tid) {
+  const int64_t col = cb * GV_COLS + tid;
+  if (col < g.n) {
+    const int64_t stride = g.m * g.n;
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      if (r >= g.m) continue;
+      float y = fold_partials(g.ws + r * g.n + col, g.nleaves, stride);
+      if (g.bias) y = y + g.bias[col];
+      g.c[r * g.n + col] = store_word(y);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&g.counter[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int BT, int MR, bool VEC>
+__global__ void __launch_bounds__(GV_THREADS) gemv_nn_kernel(GemvArgs g) {
+  constexpr int EB = GvElem<BT>::bytes;
+  constexpr int R = GvElem<BT>::rows;
+  __shared__ __attribute__((aligned(16))) char wbuf[2][GV_CHUNK];
+  __shared__ __attribute__((aligned(16))) float xbuf[2][R * MR];
+  __shared__ unsigned int last_flag;
+  set_flush_inputs_mode();
+  const int tid = threadIdx.x;
+
+  // this workgroup's items: (task, chunk), task = blockIdx.x + i * gridDim.x, leaf-major
+  // tasks (consecutive tasks are neighbouring column blocks of one leaf)
+  const int64_t my_tasks = g.ntasks > blockIdx.x ? (g.ntasks - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+  const int64_t items = my_tasks * g.chunks;
+  if (items == 0) return;  // uniform
+
+  GvStager<BT, MR, VEC> st;
+  auto task_of = [&](int64_t it) { return (int64_t)blockIdx.x + (it / g.chunks) * (int64_t)gridDim.x; };
+  {
+    const int64_t task = task_of(0);
+    st.load(g, (task % g.ncb) * GV_COLS, task / g.ncb, 0, tid);
+    st.store(wbuf[0], xbuf[0], tid);
+  }
+  __syncthreads();
+
+  float acc[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+  int64_t pending_cb = -1;        // column block of this workgroup's last counted task
+  unsigned int pending_prev = 0;  // (thread 0) the count before that task's increment
+
+  for (int64_t it = 0; it < items; ++it) {
+    const int64_t task = task_of(it);
+    const int ch = (int)(it % g.chunks);
+    const int64_t cb = task % g.ncb;
+    const int64_t t = task / g.ncb;
+    const int64_t col = cb * GV_COLS + tid;
+    if (it + 1 < items) {
+      const int64_t nt = task_of(it + 1);
+      st.load(g, (nt % g.ncb) * GV_COLS, nt / g.ncb, (int)((it + 1) % g.chunks), tid);
+    }
+    // this chunk's chain steps
+    int64_t kend = (t + 1) * g.leaf;
+    if (kend > g.k) kend = g.k;
+    int s_end = (int)(kend - (t * g.leaf + (int64_t)ch * R));
+    if (s_end > R) s_end = R;
+    const char* cur = wbuf[it & 1] + tid * EB;
+    const float* xc = xbuf[it & 1];
+    const float sc = (BT == T_I8 && col < g.n) ? g.scales[col] : 0.f;
+    for (int s = 0; s < s_end; ++s) {
+      float wv;
+      if constexpr (BT == T_F32) wv = reinterpret_cast<const float*>(cur)[s * GV_COLS];
+      else if constexpr (BT == T_BF16)
+        wv = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(cur)[s * GV_COLS] << 16);
+      else wv = (float)(int32_t)reinterpret_cast<const int8_t*>(cur)[s * GV_COLS] * sc;
+#pragma unroll
+      for (int r = 0; r < MR; ++r) acc[r] = __builtin_fmaf(xc[s * MR + r], wv, acc[r]);
+    }
+    if (ch + 1 == g.chunks) {
+      // the leaf is complete: acc is its partial
+      const bool live = col < g.n;
+      if (g.nleaves == 1) {
+        if (live) {
+          const float bj = g.bias ? g.bias[col] : 0.f;
+#pragma unroll
+          for (int r = 0; r < MR; ++r)
+            if (r < g.m) g.c[r * g.n + col] = store_word(g.bias ? acc[r] + bj : acc[r]);
+        }
+      } else {
+        if (live) {
+#pragma unroll
+          for (int r = 0; r < MR; ++r)
+            if (r < g.m)
+              __hip_atomic_store(&g.ws[(t * g.m + r) * g.n + col], acc[r], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // the agent-scope stores above are complete (device coherent) before the count
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        // the count of the previous completed task has long returned: act on it now
+        if (tid == 0) last_flag = pending_prev + 1 == (unsigned int)g.nleaves ? 1u : 0u;
+        __syncthreads();
+        if (pending_cb >= 0 && last_flag) gv_finish<MR>(g, pending_cb, tid);
+        if (tid == 0)
+          pending_prev = __hip_atomic_fetch_add(&g.counter[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pending_cb = cb;
+      }
+#pragma unroll
+      for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+    }
+    if (it + 1 < items) st.store(wbuf[(it + 1) & 1], xbuf[(it + 1) & 1], tid);
+    __syncthreads();
+  }
+  if (pending_cb >= 0) {
+    if (tid == 0) last_flag = pending_prev + 1 == (unsigned int)g.nleaves ? 1u : 0u;
+    __syncthreads();
+    if (last_flag) gv_finish<MR>(g, pending_cb, tid);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
+
+static bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
+static int elem_bytes(int t) { return t == T_F32 ? 4 : (t == T_BF16 ? 2 : 1); }
 
 static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
   // Largest power-of-two group <= 32 leaves; split further (aligned subtrees) while the
@@ -467,14 +722,49 @@ static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
   return (int)gsz;
 }
 
+// The skinny-M path takes OP_NN products with at most GV_MAXM float32 rows.
+static bool use_gemv(const GemmProblem& p) {
+  return p.op == OP_NN && p.a_type == T_F32 && p.m >= 1 && p.m <= GV_MAXM;
+}
+
 int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus) {
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
   if (P <= 1 || p.m <= 0 || p.n <= 0) return 0;
+  if (use_gemv(p)) return P > 1 ? P * p.m * p.n : 0;
   const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
   const int64_t gsz = pick_group(P, tiles, num_cus);
   const int64_t ng = (P + gsz - 1) / gsz;
   return ng > 1 ? ng * p.m * p.n : 0;
+}
+
+int64_t gemm_counter_count(const GemmProblem& p) {
+  const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
+  const int64_t P = leaf_count(p.k, L);
+  if (!use_gemv(p) || p.n <= 0 || P <= 1) return 0;
+  return (p.n + GV_COLS - 1) / GV_COLS;
+}
+
+template <int BT, int MR>
+static hipError_t launch_gemv_mr(const GemvArgs& g, bool vec, dim3 grid, hipStream_t s) {
+  if (vec) hipLaunchKernelGGL((gemv_nn_kernel<BT, MR, true>), grid, dim3(GV_THREADS), 0, s, g);
+  else hipLaunchKernelGGL((gemv_nn_kernel<BT, MR, false>), grid, dim3(GV_THREADS), 0, s, g);
+  return hipGetLastError();
+}
+
+template <int BT>
+static hipError_t launch_gemv_m(const GemvArgs& g, int64_t m, bool vec, dim3 grid, hipStream_t s) {
+  if (m <= 1) return launch_gemv_mr<BT, 1>(g, vec, grid, s);
+  if (m <= 2) return launch_gemv_mr<BT, 2>(g, vec, grid, s);
+  if (m <= 4) return launch_gemv_mr<BT, 4>(g, vec, grid, s);
+  if (m <= 8) return launch_gemv_mr<BT, 8>(g, vec, grid, s);
+  return launch_gemv_mr<BT, 16>(g, vec, grid, s);
+}
+
+static hipError_t launch_gemv_bt(const GemvArgs& g, int bt, int64_t m, bool vec, dim3 grid, hipStream_t s) {
+  if (bt == T_F32) return launch_gemv_m<T_F32>(g, m, vec, grid, s);
+  if (bt == T_BF16) return launch_gemv_m<T_BF16>(g, m, vec, grid, s);
+  return launch_gemv_m<T_I8>(g, m, vec, grid, s);
 }
 
 template <int OP, int AT, int BT>
@@ -494,10 +784,9 @@ static hipError_t launch_gemm_types(const GemmArgs& g, int at, int bt, dim3 grid
   return hipErrorInvalidValue;
 }
 
-static bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
-static int elem_bytes(int t) { return t == T_F32 ? 4 : (t == T_BF16 ? 2 : 1); }
 
-hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t stream) {
+hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int num_cus,
+                    hipStream_t stream) {
   if (p.m <= 0 || p.n <= 0) return hipSuccess;
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
@@ -506,6 +795,25 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
     hipLaunchKernelGGL(fold_groups_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0,
                        stream, p.c, (const float*)nullptr, p.bias, p.m, p.n, (int64_t)0);
     return hipGetLastError();
+  }
+  if (use_gemv(p)) {
+    GemvArgs v;
+    v.c = p.c; v.x = static_cast<const float*>(p.a); v.w = p.b; v.scales = p.scales; v.bias = p.bias;
+    v.ws = ws; v.counter = counters;
+    v.m = p.m; v.n = p.n; v.k = p.k; v.leaf = L; v.nleaves = P;
+    if (P > 1 && (ws == nullptr || counters == nullptr)) return hipErrorInvalidValue;
+    const int eb = elem_bytes(p.b_type);
+    const int rows = GV_CHUNK / (GV_COLS * eb);
+    v.chunks = (int)((L + rows - 1) / rows);
+    v.ncb = (p.n + GV_COLS - 1) / GV_COLS;
+    v.ntasks = v.ncb * P;
+    const bool vec = ((p.n * eb) % 16 == 0) && aligned(p.b, 16);
+    // persistent grid: as many 256-thread workgroups as are resident at once (LDS: 64 KB of W
+    // buffers plus x's two buffers each, two per CU while that fits in 160 KB)
+    const int64_t lds = 2 * (int64_t)GV_CHUNK + 2 * (int64_t)rows * (p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16) * 4;
+    int64_t grid = (lds * 2 <= 160 * 1024 ? 2 : 1) * (int64_t)num_cus;
+    if (grid > v.ntasks) grid = v.ntasks;
+    return launch_gemv_bt(v, p.b_type, p.m, vec, dim3((unsigned)grid), stream);
   }
   GemmArgs g;
   g.c = p.c; g.a = p.a; g.b = p.b; g.scales = p.scales; g.bias = p.bias; g.ws = ws;

@@ -116,3 +116,49 @@ def bf16_narrow(x):
     with torch.cuda.device(x.device):
         _native.check(_native.lib().mlg_bf16_narrow(out.data_ptr(), x.data_ptr(), x.numel(), _stream(x)))
     return out
+
+
+T_F32, T_BF16, T_I8 = 0, 1, 2
+
+
+def workspace_bytes(m, n, k, *, op=OP_NN, a_type=T_F32, b_type=T_F32, leaf=0):
+    """Workspace bytes `gemm_ws` needs for this product on the current device."""
+    nb = _native.lib().mlg_gemm_workspace_bytes(m, n, k, op, a_type, b_type, leaf)
+    if nb < 0:
+        _native.check(1)
+    return nb
+
+
+class Plan:
+    """One product's arguments bound once (shapes checked, workspace allocated), so that a
+    call is a single C entry with no allocation -- capturable in a HIP graph.
+
+    a: float32 (or bf16 bits with b_type=T_BF16), b: float32 / bf16 bits / int8 codes.
+    """
+
+    def __init__(self, a, b, *, op=OP_NN, scales=None, bias=None, out=None, leaf=0, b_type=None):
+        if b_type is None:
+            b_type = {torch.float32: T_F32, torch.int16: T_BF16, torch.uint16: T_BF16, torch.int8: T_I8}[b.dtype]
+        a_type = T_BF16 if a.dtype in (torch.int16, torch.uint16) else T_F32
+        if a_type == T_F32:
+            _check(a, "a", torch.float32)
+        m, n, k = _shape(a, b, op)
+        if b_type == T_I8:
+            _check(scales, "scales", torch.float32)
+            if scales.numel() != n:
+                raise ValueError(f"scales must hold n={n} values")
+        self.out = _prep_out(out, m, n, a)
+        nb = workspace_bytes(m, n, k, op=op, a_type=a_type, b_type=b_type, leaf=leaf)
+        self.ws = torch.empty(max(nb, 4), dtype=torch.uint8, device=a.device)
+        self.args = (self.out.data_ptr(), a.data_ptr(), b.data_ptr(),
+                     scales.data_ptr() if scales is not None else None, _bias(bias, n), m, n, k, op, a_type, b_type,
+                     leaf, self.ws.data_ptr(), nb)
+        self._keep = (a, b, scales, bias)
+        self._fn = _native.lib().mlg_gemm_ws
+
+    def __call__(self, stream=None):
+        s = stream.cuda_stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        rc = self._fn(*self.args, s)
+        if rc:
+            _native.check(rc)
+        return self.out

@@ -198,3 +198,80 @@ def test_bf16_conversions(oracle):
     x = _values(rng, (100000,), "special")
     n = D.bf16_narrow(torch.from_numpy(x).to(DEV)).cpu().numpy().view(np.uint16)
     assert np.array_equal(n, oracle.bf16_narrow(x))
+
+
+GEMV_SHAPES = [(1, 1, 1), (1, 255, 129), (2, 256, 128), (7, 257, 1000), (16, 1000, 4096), (1, 4100, 300),
+               (3, 4096, 4097), (16, 33, 2048), (1, 14336, 4096)]
+
+
+@pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
+@pytest.mark.parametrize("shape", GEMV_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_SHAPES])
+def test_skinny_m(oracle, shape, wt):
+    """The skinny-M (decode GEMV) path: LDS-staged W blocks, pair-of-leaves workgroups and the
+    last-arriver fold across workgroups; 16-byte and element-wise staging."""
+    D = _dev()
+    m, n, k = shape
+    rng = np.random.default_rng(m + n + k)
+    x = _values(rng, (m, k), "wide")
+    print(f"skinny {wt} m={m} n={n} k={k}", flush=True)
+    tx = torch.from_numpy(x).to(DEV)
+    if wt == "f32":
+        w = _values(rng, (k, n), "wide")
+        got = D.gemm(tx, torch.from_numpy(w).to(DEV))
+        want = oracle.gemm_fast(x, w, 0)
+    elif wt == "bf16":
+        wb = oracle.bf16_narrow(_values(rng, (k, n), "wide"))
+        got = D.gemm_bf16w(tx, torch.from_numpy(wb.view(np.int16)).to(DEV))
+        want = oracle.gemm_fast(x, oracle.bf16_widen(wb), 0)
+    else:
+        codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        got = D.gemm_int8w(tx, torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV))
+        want = oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0)
+    torch.cuda.synchronize()
+    assert_bits(got.cpu().numpy(), oracle.nan_canon(want), f"skinny {wt} {shape}")
+    # again on the same stream: the completion counters must have been left at zero
+    if wt == "i8":
+        got2 = D.gemm_int8w(tx, torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV))
+        torch.cuda.synchronize()
+        assert_bits(got2.cpu().numpy(), oracle.nan_canon(want), "second call")
+
+
+@pytest.mark.parametrize("case", ["skinny_i8", "mfma_groups", "mfma_bias"])
+def test_plan_in_graph_replays(oracle, case):
+    """A Plan (caller workspace, no allocation per call) captured in a HIP graph: every replay,
+    with eager products and synchronizations between replays, gives the oracle's bits."""
+    D = _dev()
+    rng = np.random.default_rng(77)
+    if case == "skinny_i8":
+        m, n, k = 2, 1000, 4096
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        plan = D.Plan(torch.from_numpy(a).to(DEV), torch.from_numpy(codes).to(DEV),
+                      scales=torch.from_numpy(scales).to(DEV))
+        want = oracle.gemm_fast(a, oracle.int8_dequant(codes, scales, 0), 0)
+    else:
+        m, n, k = 150, 170, 8192 if case == "mfma_groups" else 700
+        a, b = _operands(rng, m, n, k, 0, "wide")
+        bias = _values(rng, (n,), "wide") if case == "mfma_bias" else None
+        plan = D.Plan(torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV),
+                      bias=None if bias is None else torch.from_numpy(bias).to(DEV))
+        want = oracle.gemm_fast(a, b, 0)
+        if bias is not None:
+            want = oracle.bias(want, bias)
+    want = oracle.nan_canon(want)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        plan(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        plan(s)
+    for rep in range(3):
+        plan.out.fill_(-987654.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_bits(plan.out.cpu().numpy(), want, f"{case} replay {rep}")
+        gpu_gemm(*_operands(rng, 33, 40, 300, 0, "normal"), 0)  # eager work between replays
