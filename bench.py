@@ -25,14 +25,26 @@ FP32_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
 HBM_PEAK_GBS = 8000.0
 
 
+EAGER = False  # --eager: time plain launches instead of graph replays (for counter runs)
+
+
 def graph_time(calls, steps, warmup, torch):
     """Average ms per call: `steps` calls (round-robin over `calls`, each a Plan) captured in one
-    HIP graph on a private stream and replayed; HIP events on the replaying stream."""
+    HIP graph on a private stream and replayed; HIP events on the replaying stream.  With
+    EAGER the same calls are launched one by one on that stream, bracketed by its events."""
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         for i in range(max(warmup, len(calls))):
             calls[i % len(calls)](s)
     torch.cuda.synchronize()
+    if EAGER:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(steps):
+            calls[i % len(calls)](s)
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / steps
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for i in range(steps):
@@ -46,6 +58,23 @@ def graph_time(calls, steps, warmup, torch):
     e1.record(cur)
     e1.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+PREFILL_PROFILE = os.path.join(ROOT, "profiles", "gemm_mfma_kernel_prefill_2048x4096x4096.md")
+
+
+def profiled_traffic(path=PREFILL_PROFILE):
+    """HBM bytes per launch of the prefill kernel as last measured by rocprofv3 (FETCH_SIZE +
+    WRITE_SIZE, each scaled by a plain 1 GiB copy), read from the committed summary; None if
+    the summary is absent."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def _rows(m, count=8):
@@ -135,6 +164,17 @@ def cpu_baseline(W, O, min_seconds=10.0, max_seconds=30.0):
                       f"oracle/gemm_oracle.c fast arm (AVX2 FMA), {threads} threads, {dt:.1f} s"}
 
 
+def copy_calibration(torch, nbytes=1 << 30):
+    """Three copies of a 1 GiB float32 buffer (torch's elementwise copy kernel): each dispatch
+    reads and writes exactly `nbytes`, the yardstick for the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "dispatches": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +183,9 @@ def main():
     ap.add_argument("--all", action="store_true", help="also measure the other four workloads")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle comparison")
+    ap.add_argument("--eager", action="store_true", help="time eager launches, no HIP graph")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (the byte-counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -151,6 +194,12 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
+    global EAGER
+    EAGER = args.eager
 
     from mojolearn_amd import device as D
     from mojolearn_amd import workloads as W
@@ -192,7 +241,8 @@ def main():
                    "m": 2048, "n": 4096, "k": 4096, "parallelism": "none (1 GPU)"},
         "pct_of_peak": round(100.0 * pre["tflops"] / FP32_PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 3), "peak": FP32_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(pre["tflops"] / FP32_PEAK_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(pre["tflops"] / FP32_PEAK_TFLOPS, 4),
+                     "traffic": profiled_traffic()},
     }
     if check:
         line["mismatched_words"] = pre["mismatched_words"]

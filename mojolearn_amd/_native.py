@@ -90,3 +90,23 @@ def check(rc):
     """Raise RuntimeError with mlg_last_error() if a device entry failed."""
     if rc != 0:
         raise RuntimeError(lib().mlg_last_error().decode("utf-8", "replace"))
+
+
+_capsule_keep = None
+
+
+def capsule():
+    """The op table as the reference's providers export it: a PyCapsule named
+    "mojolearn.linalg.v1" whose pointer is a one-entry array holding `linalg_native_v1`
+    (gemm/linalg_dispatch.mojo:10-11,92-102; providers/python/neural_descriptor_pyapi_door.mojo:76-87).
+    The table and the name live for the life of the process, as PyCapsule borrows both."""
+    global _capsule_keep
+    L = lib()
+    if _capsule_keep is None:
+        name = ctypes.create_string_buffer(L.mlg_abi_name())
+        table = (ctypes.c_void_p * 1)(ctypes.cast(L.linalg_native_v1, ctypes.c_void_p).value)
+        new = ctypes.pythonapi.PyCapsule_New
+        new.restype = ctypes.py_object
+        new.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        _capsule_keep = (name, table, new(ctypes.addressof(table), ctypes.addressof(name), None))
+    return _capsule_keep[2]

@@ -39,6 +39,20 @@ def test_metadata_ops():
     assert p["profile"] == "mojolearn.identical.gemm.fp32.v1" and p["identity_claimed"]
 
 
+def test_capsule_carries_the_one_entry_table():
+    """The reference binds its op table as a PyCapsule named "mojolearn.linalg.v1" whose
+    pointer is an array of one C function (gemm/linalg_dispatch.mojo:92-102)."""
+    cap = _native.capsule()
+    get = ctypes.pythonapi.PyCapsule_GetPointer
+    get.restype, get.argtypes = ctypes.c_void_p, [ctypes.py_object, ctypes.c_char_p]
+    table = ctypes.cast(get(cap, b"mojolearn.linalg.v1"), ctypes.POINTER(ctypes.c_void_p))
+    assert table[0] == ctypes.cast(_native.lib().linalg_native_v1, ctypes.c_void_p).value
+    entry = ctypes.CFUNCTYPE(ctypes.c_int64, *([ctypes.c_int64] * 9 + [_native.SINK_T]))(table[0])
+    r = ctypes.c_int64(0)
+    assert entry(12, 0, 0, 0, 0, 0, 0, ctypes.addressof(r), 0, _native.SINK_T(lambda *a: None)) == 0
+    assert r.value == 1
+
+
 def test_op_table_errors_come_through_the_sink_once():
     with pytest.raises(RuntimeError, match="linalg native ABI: unknown operation"):
         _native.call(99, [], [])
