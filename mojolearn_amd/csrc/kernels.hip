@@ -51,134 +51,148 @@ __device__ __forceinline__ float store_word(float x) {
 
 // ---------------------------------------------------------------------------
 // Tiling: 512 threads = 8 waves (2 per SIMD); workgroup tile 128 x 128 cells; each
-// wave owns 64 rows x 32 columns = one v_mfma_f32_32x32x1_2b_f32 (block 0 = rows 0-31,
-// block 1 = rows 32-63, both against the same 32 columns).  K is staged through LDS
-// in KT = 32 slices, double buffered.
+// wave owns 64 rows x 32 columns = one v_mfma_f32_32x32x1_2b_f32 per k step (block 0 =
+// rows 0-31, block 1 = rows 32-63, both against the same 32 columns).  K is staged
+// through LDS in KT = 32-step slices, double buffered.  Operands travel global -> LDS
+// with global_load_lds_dwordx4 (16 bytes per lane, straight into LDS, no registers) in
+// their stored element type; bf16 widening and int8 x column-scale dequantisation
+// happen when a lane reads its MFMA operand out of LDS.
 constexpr int NTHREADS = 512;
+constexpr int NWAVES = NTHREADS / 64;
 constexpr int BM = 128;
 constexpr int BN = 128;
 constexpr int KT = 32;
-constexpr int IP = KT + 4;    // pitch of an index-major slice [128][KT] (k contiguous)
-constexpr int KP = BM + 4;    // pitch of a k-major slice [KT][128] (index contiguous)
-constexpr int SLICE = BM * IP;  // floats per operand slice buffer (>= KT * KP)
-constexpr int MAX_GROUP_LEAVES = 32;  // one group's leaves fold in registers
+constexpr int SLICE_BYTES = BM * KT * 4;  // one operand slice at float32: 16 KB
+constexpr int MAX_GROUP_LEAVES = 32;      // one group's leaves fold in registers + one LDS slot
 
-static_assert(KT * KP <= SLICE, "slice buffer");
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* gbl_vptr;
 
-// Operand staging for one KT slice of a stored row-major operand [rows][cols] of element
-// type T: 4096 elements = 1024 chunks of 4 consecutive elements along `cols`, two chunks
-// per thread.  Index-major (IMAJ) slices are [BM indices][KT k] (the operand stores k
-// contiguously); k-major slices are [KT k][BM indices].  The per-thread pointers are
-// fixed for the whole k loop (a slice only adds a uniform k offset); chunk coordinates
-// are recomputed from the thread id, which costs VALU slots the MFMA loop leaves idle
-// rather than registers it needs.
 template <int T>
-struct ElemBytes { static constexpr int v = T == T_F32 ? 4 : (T == T_BF16 ? 2 : 1); };
+struct Elem {
+  static constexpr int bytes = T == T_F32 ? 4 : (T == T_BF16 ? 2 : 1);
+  static constexpr int per16 = 16 / bytes;  // elements per 16-byte chunk
+};
 
-template <bool IMAJ>
-__device__ __forceinline__ void chunk_coords(int q, int64_t idx0, int64_t& idx, int& koff) {
-  if constexpr (IMAJ) { idx = idx0 + (q >> 3); koff = (q & 7) << 2; }
-  else { idx = idx0 + ((q & 31) << 2); koff = q >> 5; }
-}
-
+// One staged slice (BM indices x KT steps) of an operand of element type T, as
+// NCH = BM*KT*bytes/16 chunks of 16 bytes, chunk position p loaded by lane p % 64 of
+// load instruction p / 64 (a load instruction fills 1 KB of LDS, lane L at L*16).
+//  * index-major (the operand stores k contiguously: A in NN/NT, B in NT): index r owns
+//    CR = KT*bytes/16 chunks; its chunk c sits at position r*CR + (c ^ swz(r)), so the
+//    lanes of one read (consecutive r, same c) land in different banks.
+//  * k-major (the operand stores indices contiguously: B in NN/TN, A in TN): step s owns
+//    RC = BM*bytes/16 chunks holding the BM indices in order.
 template <int T, bool IMAJ>
-struct Stager {
-  const char* ptr[2];  // the chunk's first element at k = 0
-  f4 reg[2];
+struct Slice {
+  static constexpr int EB = Elem<T>::bytes;
+  static constexpr int CE = Elem<T>::per16;
+  static constexpr int NCH = BM * KT * EB / 16;  // 1024 / 512 / 256
+  static constexpr int NI = NCH / 64;            // load instructions per slice: 16 / 8 / 4
+  static constexpr int CR = KT * EB / 16;        // 8 / 4 / 2
+  static constexpr int RC = BM * EB / 16;        // 32 / 16 / 8
+  static constexpr int PER_WAVE = (NI + NWAVES - 1) / NWAVES;
 
-  __device__ __forceinline__ void init(const void* base, int64_t cols, int64_t idx0, int tid) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int64_t idx; int koff;
-      chunk_coords<IMAJ>(tid + NTHREADS * h, idx0, idx, koff);
-      const int64_t off = IMAJ ? idx * cols + koff : (int64_t)koff * cols + idx;
-      ptr[h] = static_cast<const char*>(base) + off * ElemBytes<T>::v;
-    }
-  }
+  __device__ static __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & (CR - 1); }
 
-  // Load the slice starting at k0 (uniform).  Elements outside the operand read as 0;
-  // no k step ever uses one (the step count is exact) and no store reads one (index masks).
-  __device__ __forceinline__ void load(int64_t rows, int64_t cols, int64_t idx0, int64_t k0,
-                                       bool vec, const float* scales, int tid) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int64_t idx; int koff;
-      chunk_coords<IMAJ>(tid + NTHREADS * h, idx0, idx, koff);
-      const int64_t kk = k0 + koff;
-      bool ok;
-      int64_t left;  // elements of the chunk inside the operand's row
-      const char* p;
-      if constexpr (IMAJ) {
-        ok = idx < rows && kk < cols;
-        left = cols - kk;
-        p = ptr[h] + k0 * ElemBytes<T>::v;
-      } else {
-        ok = idx < cols && kk < rows;
-        left = cols - idx;
-        p = ptr[h] + k0 * cols * ElemBytes<T>::v;
-      }
-      f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (ok) {
-        const bool full = vec && left >= 4;
-        if constexpr (T == T_F32) {
-          const float* fp = reinterpret_cast<const float*>(p);
-          if (full) {
-            v = *reinterpret_cast<const f4*>(fp);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (e < left) v[e] = fp[e];
-          }
-        } else if constexpr (T == T_BF16) {
-          const uint16_t* hp = reinterpret_cast<const uint16_t*>(p);
-          uint32_t w[4] = {0u, 0u, 0u, 0u};
-          if (full) {
-            const uint2 u = *reinterpret_cast<const uint2*>(hp);
-            w[0] = u.x & 0xFFFFu; w[1] = u.x >> 16; w[2] = u.y & 0xFFFFu; w[3] = u.y >> 16;
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (e < left) w[e] = hp[e];
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(w[e] << 16);
-        } else {
-          const int8_t* bp = reinterpret_cast<const int8_t*>(p);
-          int32_t code[4] = {0, 0, 0, 0};
-          if (full) {
-            const uint32_t u = *reinterpret_cast<const uint32_t*>(bp);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) code[e] = (int32_t)(int8_t)(u >> (8 * e));
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (e < left) code[e] = bp[e];
-          }
-          // B_eff = fl32(f32(code) * ftz(scale[j])): MODE.FP_DENORM = 2 flushes the scale on
-          // input, and the MFMA's input flush applies ftz to the product.  j is the chunk's
-          // row for an [n][k] operand and its column for a [k][n] operand.
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float sc = IMAJ ? scales[idx] : scales[idx + (e < left ? e : 0)];
-            v[e] = (float)code[e] * sc;
-          }
-        }
-      }
-      reg[h] = v;
-    }
-  }
-
-  __device__ __forceinline__ void store(float* lds, int tid) const {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int q = tid + NTHREADS * h;
-      int o;
-      if constexpr (IMAJ) o = (q >> 3) * IP + ((q & 7) << 2);
-      else o = (q >> 5) * KP + ((q & 31) << 2);
-      *reinterpret_cast<f4*>(lds + o) = reg[h];
+  // Chunk position p -> (index offset, step offset) of its first element.
+  __device__ static __forceinline__ void coords(int p, int& di, int& dk) {
+    if constexpr (IMAJ) {
+      const int r = p / CR;
+      di = r;
+      dk = ((p % CR) ^ swz(r)) * CE;
+    } else {
+      di = (p % RC) * CE;
+      dk = p / RC;
     }
   }
 };
+
+// The global side of one operand: this lane's share of every slice's load instructions.
+// `pitch` is the stored row length in elements (a multiple of 16 bytes; the base is
+// 16-byte aligned), `nidx` the operand's index count (m or n) and `krows` = k.  A chunk
+// outside the operand is read from an in-bounds chunk instead: an index past the end
+// reads the last index (its cells are never stored), a step past k reads the last stored
+// chunk (no chain step reads it), so every load is in bounds and none is predicated.
+template <int T, bool IMAJ>
+struct DirectLoader {
+  using S = Slice<T, IMAJ>;
+  const char* ptr[S::PER_WAVE];  // this lane's chunk with its step offset removed
+  int dk[S::PER_WAVE];
+
+  __device__ __forceinline__ void init(const void* base, int64_t nidx, int64_t pitch, int64_t idx0,
+                                       int wave, int lane) {
+#pragma unroll
+    for (int h = 0; h < S::PER_WAVE; ++h) {
+      const int q = wave + NWAVES * h;
+      int di, d;
+      S::coords((q < S::NI ? q : 0) * 64 + lane, di, d);
+      int64_t i = idx0 + di;
+      if constexpr (IMAJ) {
+        if (i >= nidx) i = nidx - 1;
+        ptr[h] = static_cast<const char*>(base) + i * pitch * S::EB;
+      } else {
+        if (i + S::CE > pitch) i = pitch - S::CE;
+        ptr[h] = static_cast<const char*>(base) + i * S::EB;
+      }
+      dk[h] = d;
+    }
+  }
+
+  // Issue this wave's loads of the slice that starts at step k0 into `slice`.
+  __device__ __forceinline__ void issue(char* slice, int64_t k0, int64_t pitch, int64_t krows,
+                                        int wave) const {
+#pragma unroll
+    for (int h = 0; h < S::PER_WAVE; ++h) {
+      const int q = wave + NWAVES * h;
+      if (S::NI % NWAVES != 0 && q >= S::NI) break;  // wave-uniform
+      int64_t kk = k0 + dk[h];
+      const char* src;
+      if constexpr (IMAJ) {
+        if (kk + S::CE > pitch) kk = pitch - S::CE;
+        src = ptr[h] + kk * S::EB;
+      } else {
+        if (kk >= krows) kk = krows - 1;
+        src = ptr[h] + kk * pitch * S::EB;
+      }
+      __builtin_amdgcn_global_load_lds((gbl_vptr)src, (lds_vptr)(slice + q * 1024), 16, 0, 0);
+    }
+  }
+};
+
+// A lane's MFMA operand values for steps s .. s+3 of a staged slice, as float32: index
+// `idx` of the slice.  bf16 widens exactly (bits << 16); int8 is f32(code) * scale, one
+// rounding, the scale flushed on input by MODE.FP_DENORM = 2 (and the product by the
+// MFMA's input flush), i.e. ftz(f32(code) * ftz(scale)).
+template <int T, bool IMAJ>
+__device__ __forceinline__ f4 read4(const char* slice, int idx, int s, float scale) {
+  using S = Slice<T, IMAJ>;
+  f4 v;
+  if constexpr (IMAJ) {
+    const int c = s * S::EB / 16;              // chunk holding step s
+    const int sub = (s * S::EB) % 16;          // byte offset of step s in it
+    const char* p = slice + (idx * S::CR + (c ^ S::swz(idx))) * 16 + sub;
+    if constexpr (T == T_F32) {
+      v = *reinterpret_cast<const f4*>(p);
+    } else if constexpr (T == T_BF16) {
+      const uint2 u = *reinterpret_cast<const uint2*>(p);
+      v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xFFFF0000u);
+      v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xFFFF0000u);
+    } else {
+      const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (float)(int32_t)(int8_t)(u >> (8 * e)) * scale;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const char* p = slice + ((s + e) * BM + idx) * S::EB;
+      if constexpr (T == T_F32) v[e] = *reinterpret_cast<const float*>(p);
+      else if constexpr (T == T_BF16) v[e] = __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(p) << 16);
+      else v[e] = (float)*reinterpret_cast<const int8_t*>(p) * scale;
+    }
+  }
+  return v;
+}
 
 __device__ __forceinline__ v32f vadd(const v32f& x, const v32f& y) {
   v32f r;
@@ -211,8 +225,9 @@ struct Stack32 {
     return x;
   }
   // Push partial number t (0-based, t <= 30): merge slot l while bit l of t is 1, then
-  // store into the first slot whose bit is 0.
-  __device__ __forceinline__ void push(v32f x, int t) {
+  // store into the first slot whose bit is 0.  x is used as the running sum (its value is
+  // not needed afterwards).
+  __device__ __forceinline__ void push(v32f& x, int t) {
     if (!(t & 1)) { s0 = x; return; }
     x = vadd(s0, x);
     if (!(t & 2)) { s1 = x; return; }
@@ -237,7 +252,7 @@ struct Stack32 {
 
 struct GemmArgs {
   float* c;
-  const void* a;
+  const void* a;      // stored operands: 16-byte aligned, rows a multiple of 16 bytes
   const void* b;
   const float* scales;
   const float* bias;
@@ -247,49 +262,33 @@ struct GemmArgs {
   int64_t nleaves;    // P
   int64_t group;      // leaves per group (power of two, <= 32)
   int64_t ngroups;
-  int64_t a_rows, a_cols, b_rows, b_cols;  // stored shapes
+  int64_t a_pitch, b_pitch;  // stored row lengths in elements
   int tiles_n;
-  int a_vec, b_vec;
 };
 
-template <int OP>
-__device__ __forceinline__ void load_group(f4& a4, f4& b4, const float* la, const float* lb, int s,
-                                           int arow, int bcol) {
+// MFMA steps s0 .. s1-1 of one staged slice, in ascending order.  The slice is walked in
+// aligned groups of 4 steps whose operands are read from LDS one group ahead; unless FULL,
+// a step outside [s0, s1) is skipped by a uniform branch.  The scheduling fences keep the
+// compiler from hoisting every LDS read of the slice, which would not fit beside the
+// accumulator and the fold slots.
+template <int OP, int AT, int BT, bool FULL>
+__device__ __forceinline__ void mfma_steps(v32f& acc, const char* la, const char* lb, int s0, int s1,
+                                           int arow, int bcol, float scale) {
   constexpr bool A_IMAJ = (OP != OP_TN);
   constexpr bool B_IMAJ = (OP == OP_NT);
-  if constexpr (A_IMAJ) {
-    a4 = *reinterpret_cast<const f4*>(la + arow * IP + s);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) a4[q] = la[(s + q) * KP + arow];
-  }
-  if constexpr (B_IMAJ) {
-    b4 = *reinterpret_cast<const f4*>(lb + bcol * IP + s);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) b4[q] = lb[(s + q) * KP + bcol];
-  }
-}
-
-// MFMA steps s0 .. s1-1 of one staged K slice, in ascending order.  One code path for
-// full and ragged slices (a separate loop for ragged ones gets its own copy of the
-// accumulator): the slice is walked in aligned groups of 4 steps whose operands are
-// read from LDS one group ahead, and a step outside [s0, s1) is skipped by a uniform
-// branch.  The scheduling fences keep the compiler from hoisting every LDS read of the
-// slice, which would not fit beside the accumulator and the fold slots.
-template <int OP>
-__device__ __forceinline__ void mfma_steps(v32f& acc, const float* la, const float* lb, int s0,
-                                           int s1, int arow, int bcol) {
-  f4 a4, b4;
-  load_group<OP>(a4, b4, la, lb, 0, arow, bcol);
+  f4 a4 = read4<AT, A_IMAJ>(la, arow, 0, 1.f);
+  f4 b4 = read4<BT, B_IMAJ>(lb, bcol, 0, scale);
 #pragma unroll
   for (int s = 0; s < KT; s += 4) {
     f4 an, bn;
-    if (s + 4 < KT) load_group<OP>(an, bn, la, lb, s + 4, arow, bcol);
+    if (s + 4 < KT) {
+      an = read4<AT, A_IMAJ>(la, arow, s + 4, 1.f);
+      bn = read4<BT, B_IMAJ>(lb, bcol, s + 4, scale);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (s + q >= s0 && s + q < s1) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[q], b4[q], acc, 0, 0, 0);
+      if (FULL || (s + q >= s0 && s + q < s1)) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[q], b4[q], acc, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     if (s + 4 < KT) { a4 = an; b4 = bn; }
   }
@@ -299,8 +298,8 @@ template <int OP, int AT, int BT>
 __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   constexpr bool A_IMAJ = (OP != OP_TN);
   constexpr bool B_IMAJ = (OP == OP_NT);
-  __shared__ float lds[2][2][SLICE];  // [buffer][A,B][slice]
-  __shared__ f4 slot4[NTHREADS / 64][8][64];  // fold slot 4, per wave
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][SLICE_BYTES];  // [buffer][A,B]
+  __shared__ f4 slot4[NWAVES][8][64];  // fold slot 4, per wave
 
   set_flush_inputs_mode();
 
@@ -326,18 +325,21 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   const int64_t kt_first = kb / KT;
   const int64_t kt_last = (ke - 1) / KT;
 
-  Stager<AT, A_IMAJ> sa;
-  Stager<BT, B_IMAJ> sb;
-  sa.init(g.a, g.a_cols, i0, tid);
-  sb.init(g.b, g.b_cols, j0, tid);
-  sa.load(g.a_rows, g.a_cols, i0, kt_first * KT, g.a_vec != 0, nullptr, tid);
-  sb.load(g.b_rows, g.b_cols, j0, kt_first * KT, g.b_vec != 0, g.scales, tid);
-  sa.store(lds[0][0], tid);
-  sb.store(lds[0][1], tid);
-  __syncthreads();
+  DirectLoader<AT, A_IMAJ> lda;
+  DirectLoader<BT, B_IMAJ> ldb;
+  lda.init(g.a, g.m, g.a_pitch, i0, wave, lane);
+  ldb.init(g.b, g.n, g.b_pitch, j0, wave, lane);
+  lda.issue(lds[0][0], kt_first * KT, g.a_pitch, g.k, wave);
+  ldb.issue(lds[0][1], kt_first * KT, g.b_pitch, g.k, wave);
 
   const int arow = wr * 64 + lane;
   const int bcol = wc * 32 + (lane & 31);
+  float scale = 1.f;
+  if constexpr (BT == T_I8) {
+    int64_t j = j0 + bcol;
+    if (j >= g.n) j = g.n - 1;
+    scale = g.scales[j];
+  }
 
   v32f acc;
 #pragma unroll
@@ -349,22 +351,28 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   int64_t leaf_end = (t_first + 1) * g.leaf;
   if (leaf_end > g.k) leaf_end = g.k;
 
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's slice loads have landed
+  __syncthreads();
+
   int buf = 0;
   for (int64_t kt = kt_first; kt <= kt_last; ++kt) {
-    const bool more = kt < kt_last;
-    if (more) {
-      sa.load(g.a_rows, g.a_cols, i0, (kt + 1) * KT, g.a_vec != 0, nullptr, tid);
-      sb.load(g.b_rows, g.b_cols, j0, (kt + 1) * KT, g.b_vec != 0, g.scales, tid);
+    if (kt < kt_last) {
+      // The other buffer was last read before the barrier that ended the previous slice.
+      lda.issue(lds[buf ^ 1][0], (kt + 1) * KT, g.a_pitch, g.k, wave);
+      ldb.issue(lds[buf ^ 1][1], (kt + 1) * KT, g.b_pitch, g.k, wave);
     }
-    const float* la = lds[buf][0];
-    const float* lb = lds[buf][1];
+    const char* la = lds[buf][0];
+    const char* lb = lds[buf][1];
     const int64_t tbase = kt * KT;
     int64_t pos = tbase > kb ? tbase : kb;
     int64_t hi = tbase + KT;
     if (hi > ke) hi = ke;
     while (pos < hi) {
       const int64_t seg = hi < leaf_end ? hi : leaf_end;
-      mfma_steps<OP>(acc, la, lb, (int)(pos - tbase), (int)(seg - tbase), arow, bcol);
+      if (pos == tbase && seg == tbase + KT)
+        mfma_steps<OP, AT, BT, true>(acc, la, lb, 0, KT, arow, bcol, scale);
+      else
+        mfma_steps<OP, AT, BT, false>(acc, la, lb, (int)(pos - tbase), (int)(seg - tbase), arow, bcol, scale);
       pos = seg;
       if (pos == leaf_end) {
         if (t + 1 < cnt) {
@@ -379,15 +387,12 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
         }
       }
     }
-    if (more) {
-      sa.store(lds[buf ^ 1][0], tid);
-      sb.store(lds[buf ^ 1][1], tid);
-    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next slice's loads have landed
     __syncthreads();
     buf ^= 1;
   }
 
-  // acc holds the group root.  Store: acc element e -> block b = e/16, row (e%4) + 8*((e%16)/4) + 4*(lane/32) within it.
+  // acc holds the group root.  Element e -> block b = e/16, row (e%4) + 8*((e%16)/4) + 4*(lane/32) within it.
   const int64_t col = j0 + bcol;
   if (col < g.n) {
     if (g.ngroups == 1) {
@@ -411,6 +416,23 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
         if (row < g.m) wsg[row * g.n + col] = acc[e];
       }
     }
+  }
+}
+
+// Copy a stored operand [rows][cols] of `eb`-byte elements into [rows][pitch] (pitch a
+// multiple of 16 bytes, zero padding), so that the product kernel's 16-byte loads are
+// aligned and never straddle a row end.
+__global__ void repack_rows_kernel(char* dst, const char* src, int64_t rows, int64_t cols, int64_t pitch,
+                                   int eb) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * pitch) return;
+  const int64_t r = i / pitch, cidx = i % pitch;
+  if (eb == 4) {
+    reinterpret_cast<uint32_t*>(dst)[i] = cidx < cols ? reinterpret_cast<const uint32_t*>(src)[r * cols + cidx] : 0u;
+  } else if (eb == 2) {
+    reinterpret_cast<uint16_t*>(dst)[i] = cidx < cols ? reinterpret_cast<const uint16_t*>(src)[r * cols + cidx] : (uint16_t)0;
+  } else {
+    dst[i] = cidx < cols ? src[r * cols + cidx] : (char)0;
   }
 }
 
@@ -727,15 +749,39 @@ static bool use_gemv(const GemmProblem& p) {
   return p.op == OP_NN && p.a_type == T_F32 && p.m >= 1 && p.m <= GV_MAXM;
 }
 
+// Stored shape of an operand of the MFMA path: [rows][cols] elements.
+static void stored_shape(const GemmProblem& p, bool is_a, int64_t& rows, int64_t& cols) {
+  if (is_a) {
+    if (p.op == OP_TN) { rows = p.k; cols = p.m; } else { rows = p.m; cols = p.k; }
+  } else {
+    if (p.op == OP_NT) { rows = p.n; cols = p.k; } else { rows = p.k; cols = p.n; }
+  }
+}
+
+// Floats of workspace the MFMA path needs to repack an operand whose base is not 16-byte
+// aligned or whose rows are not a multiple of 16 bytes (0 when it is loaded in place).
+static int64_t repack_floats(const GemmProblem& p, bool is_a) {
+  int64_t rows, cols;
+  stored_shape(p, is_a, rows, cols);
+  const int eb = elem_bytes(is_a ? p.a_type : p.b_type);
+  const void* base = is_a ? p.a : p.b;
+  if ((cols * eb) % 16 == 0 && (base == nullptr || aligned(base, 16))) return 0;
+  const int64_t ce = 16 / eb;
+  const int64_t pitch = (cols + ce - 1) / ce * ce;
+  return (rows * pitch * eb + 255) / 256 * 64;  // 256-byte granules
+}
+
+static int64_t round_floats(int64_t f) { return (f + 63) / 64 * 64; }
+
 int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus) {
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
-  if (P <= 1 || p.m <= 0 || p.n <= 0) return 0;
+  if (P < 1 || p.m <= 0 || p.n <= 0) return 0;
   if (use_gemv(p)) return P > 1 ? P * p.m * p.n : 0;
   const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
-  const int64_t gsz = pick_group(P, tiles, num_cus);
+  const int64_t gsz = P > 1 ? pick_group(P, tiles, num_cus) : 1;
   const int64_t ng = (P + gsz - 1) / gsz;
-  return ng > 1 ? ng * p.m * p.n : 0;
+  return (ng > 1 ? round_floats(ng * p.m * p.n) : 0) + repack_floats(p, true) + repack_floats(p, false);
 }
 
 int64_t gemm_counter_count(const GemmProblem& p) {
@@ -818,17 +864,34 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
   GemmArgs g;
   g.c = p.c; g.a = p.a; g.b = p.b; g.scales = p.scales; g.bias = p.bias; g.ws = ws;
   g.m = p.m; g.n = p.n; g.k = p.k; g.leaf = L; g.nleaves = P;
-  if (p.op == OP_TN) { g.a_rows = p.k; g.a_cols = p.m; } else { g.a_rows = p.m; g.a_cols = p.k; }
-  if (p.op == OP_NT) { g.b_rows = p.n; g.b_cols = p.k; } else { g.b_rows = p.k; g.b_cols = p.n; }
-  const int ea = elem_bytes(p.a_type), eb = elem_bytes(p.b_type);
-  g.a_vec = (g.a_cols % 4 == 0) && aligned(p.a, 4 * ea);
-  g.b_vec = (g.b_cols % 4 == 0) && aligned(p.b, 4 * eb);
   const int64_t tm = (p.m + BM - 1) / BM, tn = (p.n + BN - 1) / BN;
   g.tiles_n = (int)tn;
   const int64_t gsz = P > 1 ? pick_group(P, tm * tn, num_cus) : 1;
   g.group = gsz;
   g.ngroups = (P + gsz - 1) / gsz;
-  if (g.ngroups > 1 && ws == nullptr) return hipErrorInvalidValue;
+  // workspace: [group roots][A repacked][B repacked], each part 256-byte aligned
+  float* wsp = ws + (g.ngroups > 1 ? round_floats(g.ngroups * p.m * p.n) : 0);
+  const int64_t ra = repack_floats(p, true), rb = repack_floats(p, false);
+  if ((g.ngroups > 1 || ra > 0 || rb > 0) && ws == nullptr) return hipErrorInvalidValue;
+  for (int which = 0; which < 2; ++which) {
+    const bool is_a = which == 0;
+    int64_t rows, cols;
+    stored_shape(p, is_a, rows, cols);
+    const int eb = elem_bytes(is_a ? p.a_type : p.b_type);
+    const int64_t ce = 16 / eb;
+    const int64_t pitch = (cols + ce - 1) / ce * ce;
+    const void* src = is_a ? p.a : p.b;
+    if ((is_a ? ra : rb) > 0) {
+      const int64_t total = rows * pitch;
+      hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                         (char*)wsp, (const char*)src, rows, cols, pitch, eb);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      src = wsp;
+      wsp += is_a ? ra : rb;
+    }
+    if (is_a) { g.a = src; g.a_pitch = pitch; } else { g.b = src; g.b_pitch = pitch; }
+  }
   dim3 grid((unsigned)(tm * tn), (unsigned)g.ngroups);
   hipError_t e;
   if (p.op == OP_NN) e = launch_gemm_types<OP_NN>(g, p.a_type, p.b_type, grid, stream);
