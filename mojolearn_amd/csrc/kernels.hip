@@ -480,126 +480,54 @@ __global__ void __launch_bounds__(256) fold_groups_kernel(float* c, const float*
 // ---------------------------------------------------------------------------
 // Skinny-M product (decode GEMV), OP_NN: X[M x K] . W[K x N], M <= 16.
 //
-// Work is split into tasks: (block of 256 output columns, one k-leaf).  A persistent grid of
-// 256-thread workgroups walks its tasks leaf chunk by leaf chunk through one continuous
-// pipeline: the 256 threads stream the next chunk of W (R rows x 256 columns, 16-byte loads,
-// 32 KB) and of x into registers while the current chunk's chains run out of LDS, so HBM sees
-// a steady stream regardless of how the serial chains are owned.  Thread c runs the chain of
-// column c: a VALU FMA per step under MODE.FP_DENORM = 2 (v_fma_f32 is fma(ftz a, ftz b,
-// ftz acc), like the K=1 MFMA), for all M rows.  A finished leaf partial is published with
-// agent-scope atomic stores (device coherent, so no cache writeback is needed: the stores only
-// have to be complete before the count), counted on its column block's counter, and the task
-// that completes a block folds its P partials with the contract's tree, writes the output and
-// resets the counter.  One launch computes the whole product.
+// A wave owns one k-leaf of one column group.  Each lane owns CPL = 4 / bytes consecutive
+// columns: one 32-bit word of W per k row (4 int8 codes, 2 bf16 or 1 float32), so the 64
+// lanes read 256 contiguous bytes of every W row.  The leaf's rows stream into registers
+// GV_CH at a time, two buffers requested before the first arithmetic (a whole 128-row leaf
+// is in flight at once), and each lane runs CPL x M serial chains in VALU (v_fma_f32 under
+// MODE.FP_DENORM = 2 is fma(ftz a, ftz b, ftz acc), like the K=1 MFMA).  x is the same for
+// every lane and is read with uniform loads.  A 256-thread workgroup is one column group's
+// aligned group of GV_LEAVES leaves -- a subtree of the fold -- whose root it forms through
+// LDS.  With more than one group, the roots go to the workspace with agent-scope atomic
+// stores and are counted on the column group's counter; the workgroup that completes the
+// count folds them (the rest of the contract's tree), writes the output and resets the
+// counter.  One launch computes the whole product.
 constexpr int GV_THREADS = 256;
-constexpr int GV_COLS = 256;                // columns per task: one per thread
+constexpr int GV_LEAVES = GV_THREADS / 64;  // leaves per workgroup: an aligned subtree
 constexpr int GV_MAXM = 16;
-constexpr int GV_CHUNK = 32768;             // bytes of W per LDS buffer
-constexpr int GV_FOLD_BATCH = 32;           // partial loads in flight while folding
+constexpr int GV_CH = 128;                  // W rows per register buffer: a whole contract leaf
+constexpr int GV_FOLD_BATCH = 32;           // root loads in flight while folding
+constexpr int GV_FEW_GROUPS = 8;            // up to this many groups: all roots loaded at once
 
 template <int T>
-struct GvElem {
-  static constexpr int bytes = T == T_F32 ? 4 : (T == T_BF16 ? 2 : 1);
-  static constexpr int rows = GV_CHUNK / (GV_COLS * bytes);  // rows per chunk: 128 / 64 / 32
+struct GvCols {
+  static constexpr int cpl = 4 / Elem<T>::bytes;  // columns per lane
+  static constexpr int cols = 64 * cpl;           // columns per group
 };
 
 struct GemvArgs {
   float* c;
-  const float* x;
   const void* w;
   const float* scales;
   const float* bias;
-  float* ws;              // [nleaves][m][n] leaf partials when nleaves > 1
-  unsigned int* counter;  // [column blocks], zero between launches
+  float* ws;              // [ngroups][m][n] group roots when ngroups > 1
+  unsigned int* counter;  // [ncg], zero between launches (ngroups > 1)
   int64_t m, n, k, leaf, nleaves;
-  int64_t ncb;            // column blocks
-  int64_t ntasks;         // ncb * nleaves
-  int chunks;             // chunks per leaf: ceil(leaf / rows)
+  int64_t ngroups;        // ceil(nleaves / GV_LEAVES)
+  int64_t ncg;            // column groups
 };
 
-// Issue every global read of one chunk into registers; `store` writes them to LDS.  A
-// segment no chain step reads (a row outside the leaf, columns past n) is read from the
-// operand's first bytes instead -- an in-bounds address -- so the loads carry no branch and
-// are all in flight together; those LDS bytes only reach cells that are never stored.
-template <int T, int MR, bool VEC>
-struct GvStager {
-  static constexpr int EB = GvElem<T>::bytes;
-  static constexpr int R = GvElem<T>::rows;
-  static constexpr int SEGS = GV_COLS * EB / 16;           // 16-byte segments per row
-  static constexpr int PER = R * SEGS / GV_THREADS;        // segments per thread: 8
-  static constexpr int XPER = (R * MR + GV_THREADS - 1) / GV_THREADS;
-  u4 wv[PER];
-  float xv[XPER];
-
-  __device__ __forceinline__ void load(const GemvArgs& g, int64_t j0, int64_t t, int ch, int tid) {
-    const char* wb = static_cast<const char*>(g.w);
-    const int64_t kb = t * g.leaf + (int64_t)ch * R;
-    int64_t kend = (t + 1) * g.leaf;
-    if (kend > g.k) kend = g.k;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int q = tid + i * GV_THREADS;
-      const int rr = q / SEGS;
-      const int sg = q % SEGS;
-      const int64_t kk = kb + rr;
-      const int64_t col = j0 + (int64_t)sg * (16 / EB);
-      if constexpr (VEC) {
-        const bool ok = kk < kend && col < g.n;
-        wv[i] = *reinterpret_cast<const u4*>(ok ? wb + (kk * g.n + col) * EB : wb);
-      } else {
-        u4 v = {0u, 0u, 0u, 0u};
-        if (kk < kend) {
-          const char* src = wb + (kk * g.n + col) * EB;
-          char* d = reinterpret_cast<char*>(&v);
-#pragma unroll
-          for (int e = 0; e < 16 / EB; ++e)
-            if (col + e < g.n) {
-              if constexpr (EB == 4) reinterpret_cast<float*>(d)[e] = reinterpret_cast<const float*>(src)[e];
-              else if constexpr (EB == 2) reinterpret_cast<uint16_t*>(d)[e] = reinterpret_cast<const uint16_t*>(src)[e];
-              else d[e] = src[e];
-            }
-        }
-        wv[i] = v;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < XPER; ++i) {
-      const int q = tid + i * GV_THREADS;
-      const int rr = q / MR;
-      const int r = q % MR;
-      const int64_t kk = kb + rr;
-      const bool ok = q < R * MR && kk < kend && r < g.m;
-      xv[i] = *(ok ? g.x + r * g.k + kk : g.x);  // rows past m feed cells that are never stored
-    }
-  }
-
-  __device__ __forceinline__ void store(char* buf, float* xbuf, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int q = tid + i * GV_THREADS;
-      *reinterpret_cast<u4*>(buf + (q / SEGS) * GV_COLS * EB + (q % SEGS) * 16) = wv[i];
-    }
-#pragma unroll
-    for (int i = 0; i < XPER; ++i) {
-      const int q = tid + i * GV_THREADS;
-      if (q < R * MR) xbuf[q] = xv[i];
-    }
-  }
-};
-
-// The contract's tree over a cell's P leaf partials ws[t * stride], read with agent-scope
-// atomic loads issued GV_FOLD_BATCH at a time.
-__device__ __forceinline__ float fold_partials(const float* base, int64_t P, int64_t stride) {
+// The contract's tree over a cell's P roots base[t * stride], read with agent-scope atomic
+// loads issued up to GV_FOLD_BATCH at a time.
+__device__ __forceinline__ float fold_roots(const float* base, int64_t P, int64_t stride) {
   StackF stk;
   int64_t t = 0;
   float last = 0.f;
   for (int64_t t0 = 0; t0 < P; t0 += GV_FOLD_BATCH) {
     float v[GV_FOLD_BATCH];
 #pragma unroll
-    for (int e = 0; e < GV_FOLD_BATCH; ++e) {
-      const int64_t tt = t0 + e < P ? t0 + e : P - 1;
-      v[e] = __hip_atomic_load(base + tt * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int e = 0; e < GV_FOLD_BATCH; ++e)
+      if (t0 + e < P) v[e] = __hip_atomic_load(base + (t0 + e) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
     for (int e = 0; e < GV_FOLD_BATCH; ++e) {
       if (t0 + e >= P) break;
@@ -611,121 +539,339 @@ __device__ __forceinline__ float fold_partials(const float* base, int64_t P, int
   return stk.root(last, (int)t);
 }
 
-// The task that completed column block `cb`: fold each cell's P partials, write the output,
-// reset the block's counter.
-template <int MR>
-__device__ __forceinline__ void gv_finish(const GemvArgs& g, int64_t cb, int tid) {
-  const int64_t col = cb * GV_COLS + tid;
-  if (col < g.n) {
-    const int64_t stride = g.m * g.n;
+// Word 3 of a raw buffer resource on gfx9-family targets (32-bit data format, no swizzle).
+constexpr int GV_RSRC_WORD3 = 0x00020000;
+
+// Load the words of rows k0 .. k0+GV_CH-1 (rows past `klast` read row `klast`: in bounds,
+// and no chain step uses them).  VEC: buffer loads, the chunk's first row in a scalar
+// resource, the row offset i*rowbytes in the scalar offset and the lane's byte offset
+// `loff` in one VGPR (the host keeps GV_CH * rowbytes below 2^31).  Otherwise one load per
+// element at the per-column offsets `coff`.
+template <int BT, bool VEC>
+__device__ __forceinline__ void gv_load(uint32_t (&buf)[GV_CH], const char* w, uint32_t loff, const uint32_t* coff,
+                                        int64_t rowbytes, int64_t k0, int64_t klast) {
+  const int64_t last = klast - k0;  // >= GV_CH - 1 for a full chunk
+  if constexpr (VEC) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(w + k0 * rowbytes), (short)0, 0x7FFFFFFF, GV_RSRC_WORD3);
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-      if (r >= g.m) continue;
-      float y = fold_partials(g.ws + r * g.n + col, g.nleaves, stride);
-      if (g.bias) y = y + g.bias[col];
-      g.c[r * g.n + col] = store_word(y);
+    for (int i = 0; i < GV_CH; ++i) {
+      const int ii = i <= last ? i : (int)last;
+      buf[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ii * (int)rowbytes, 0);
+    }
+  } else {
+    constexpr int CPL = GvCols<BT>::cpl;
+#pragma unroll
+    for (int i = 0; i < GV_CH; ++i) {
+      const int64_t ii = i <= last ? i : last;
+      const char* row = w + (k0 + ii) * rowbytes;
+      uint32_t u = 0;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        if constexpr (BT == T_F32) u = *reinterpret_cast<const uint32_t*>(row + coff[e]);
+        else if constexpr (BT == T_BF16) u |= (uint32_t)*reinterpret_cast<const uint16_t*>(row + coff[e]) << (16 * e);
+        else u |= (uint32_t)*reinterpret_cast<const uint8_t*>(row + coff[e]) << (8 * e);
+      }
+      buf[i] = u;
     }
   }
-  if (tid == 0) __hip_atomic_store(&g.counter[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int BT, int MR, bool VEC>
-__global__ void __launch_bounds__(GV_THREADS) gemv_nn_kernel(GemvArgs g) {
-  constexpr int EB = GvElem<BT>::bytes;
-  constexpr int R = GvElem<BT>::rows;
-  __shared__ __attribute__((aligned(16))) char wbuf[2][GV_CHUNK];
-  __shared__ __attribute__((aligned(16))) float xbuf[2][R * MR];
-  __shared__ unsigned int last_flag;
-  set_flush_inputs_mode();
-  const int tid = threadIdx.x;
-
-  // this workgroup's items: (task, chunk), task = blockIdx.x + i * gridDim.x, leaf-major
-  // tasks (consecutive tasks are neighbouring column blocks of one leaf)
-  const int64_t my_tasks = g.ntasks > blockIdx.x ? (g.ntasks - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-  const int64_t items = my_tasks * g.chunks;
-  if (items == 0) return;  // uniform
-
-  GvStager<BT, MR, VEC> st;
-  auto task_of = [&](int64_t it) { return (int64_t)blockIdx.x + (it / g.chunks) * (int64_t)gridDim.x; };
-  {
-    const int64_t task = task_of(0);
-    st.load(g, (task % g.ncb) * GV_COLS, task / g.ncb, 0, tid);
-    st.store(wbuf[0], xbuf[0], tid);
-  }
-  __syncthreads();
-
-  float acc[MR];
+// x values for steps k0+i0 .. k0+i0+XB-1 of every row (uniform loads; a row past m reads
+// row m-1 and a step past k reads step k-1 -- in bounds, and no chain step uses them).
+template <int MR, int XB, bool FULL>
+__device__ __forceinline__ void gv_load_x(float (&xv)[MR][XB], const float* __restrict__ x, int64_t k, int64_t k0,
+                                          int i0, int m) {
 #pragma unroll
-  for (int r = 0; r < MR; ++r) acc[r] = 0.f;
-  int64_t pending_cb = -1;        // column block of this workgroup's last counted task
-  unsigned int pending_prev = 0;  // (thread 0) the count before that task's increment
-
-  for (int64_t it = 0; it < items; ++it) {
-    const int64_t task = task_of(it);
-    const int ch = (int)(it % g.chunks);
-    const int64_t cb = task % g.ncb;
-    const int64_t t = task / g.ncb;
-    const int64_t col = cb * GV_COLS + tid;
-    if (it + 1 < items) {
-      const int64_t nt = task_of(it + 1);
-      st.load(g, (nt % g.ncb) * GV_COLS, nt / g.ncb, (int)((it + 1) % g.chunks), tid);
-    }
-    // this chunk's chain steps
-    int64_t kend = (t + 1) * g.leaf;
-    if (kend > g.k) kend = g.k;
-    int s_end = (int)(kend - (t * g.leaf + (int64_t)ch * R));
-    if (s_end > R) s_end = R;
-    const char* cur = wbuf[it & 1] + tid * EB;
-    const float* xc = xbuf[it & 1];
-    const float sc = (BT == T_I8 && col < g.n) ? g.scales[col] : 0.f;
-    for (int s = 0; s < s_end; ++s) {
-      float wv;
-      if constexpr (BT == T_F32) wv = reinterpret_cast<const float*>(cur)[s * GV_COLS];
-      else if constexpr (BT == T_BF16)
-        wv = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(cur)[s * GV_COLS] << 16);
-      else wv = (float)(int32_t)reinterpret_cast<const int8_t*>(cur)[s * GV_COLS] * sc;
+  for (int r = 0; r < MR; ++r) {
+    const float* xr = x + (r < m ? r : m - 1) * k;
 #pragma unroll
-      for (int r = 0; r < MR; ++r) acc[r] = __builtin_fmaf(xc[s * MR + r], wv, acc[r]);
-    }
-    if (ch + 1 == g.chunks) {
-      // the leaf is complete: acc is its partial
-      const bool live = col < g.n;
-      if (g.nleaves == 1) {
-        if (live) {
-          const float bj = g.bias ? g.bias[col] : 0.f;
-#pragma unroll
-          for (int r = 0; r < MR; ++r)
-            if (r < g.m) g.c[r * g.n + col] = store_word(g.bias ? acc[r] + bj : acc[r]);
-        }
+    for (int q = 0; q < XB; ++q) {
+      if constexpr (FULL) {
+        xv[r][q] = xr[k0 + i0 + q];  // a full chunk lies inside the leaf
       } else {
-        if (live) {
+        const int64_t kk = k0 + i0 + q < k ? k0 + i0 + q : k - 1;
+        xv[r][q] = xr[kk];
+      }
+    }
+  }
+}
+
+// Chain steps for rows k0 .. k0+nrows-1 (all GV_CH when FULL).  W[p, j] as float32: bf16
+// widened exactly; int8 f32(code) * scale[j], one rounding (the scale flushed on input).
+// x is read XB steps at a time, one batch ahead.
+template <int BT, int MR, bool FULL>
+__device__ __forceinline__ void gv_steps(float (&acc)[MR][GvCols<BT>::cpl], const uint32_t (&buf)[GV_CH],
+                                         const float* __restrict__ x, int64_t k, int64_t k0, int nrows,
+                                         int m, const float (&sc)[GvCols<BT>::cpl]) {
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int XB = MR >= 16 ? 1 : 16 / MR;
+  float xc[MR][XB], xn[MR][XB];
+  gv_load_x<MR, XB, FULL>(xc, x, k, k0, 0, m);
 #pragma unroll
-          for (int r = 0; r < MR; ++r)
-            if (r < g.m)
-              __hip_atomic_store(&g.ws[(t * g.m + r) * g.n + col], acc[r], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-        }
-        // the agent-scope stores above are complete (device coherent) before the count
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        // the count of the previous completed task has long returned: act on it now
-        if (tid == 0) last_flag = pending_prev + 1 == (unsigned int)g.nleaves ? 1u : 0u;
-        __syncthreads();
-        if (pending_cb >= 0 && last_flag) gv_finish<MR>(g, pending_cb, tid);
-        if (tid == 0)
-          pending_prev = __hip_atomic_fetch_add(&g.counter[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        pending_cb = cb;
+  for (int b = 0; b < GV_CH / XB; ++b) {
+    if (b + 1 < GV_CH / XB) gv_load_x<MR, XB, FULL>(xn, x, k, k0, (b + 1) * XB, m);
+#pragma unroll
+    for (int q = 0; q < XB; ++q) {
+      const int i = b * XB + q;
+      if (!FULL && i >= nrows) continue;  // uniform
+      const uint32_t u = buf[i];
+      float wv[CPL];
+      if constexpr (BT == T_F32) {
+        wv[0] = __uint_as_float(u);
+      } else if constexpr (BT == T_BF16) {
+        wv[0] = __uint_as_float(u << 16);
+        wv[1] = __uint_as_float(u & 0xFFFF0000u);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[e] = (float)((int32_t)(u << (24 - 8 * e)) >> 24) * sc[e];
+      }
+      // rows past m (MR rounds m up) run on row m-1's x and are never stored
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) acc[r][e] = __builtin_fmaf(xc[r][q], wv[e], acc[r][e]);
+    }
+    if (b + 1 < GV_CH / XB) {
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int q = 0; q < XB; ++q) xc[r][q] = xn[r][q];
+    }
+  }
+}
+
+// One whole 128-row leaf (the decode shapes: L = 128, k a multiple of 128), straight-line:
+// the rows travel in blocks of GV_RB through a ring of GV_AHEAD + 1 register blocks, GV_AHEAD
+// blocks requested ahead of the one being consumed, so the wave keeps loads in flight while
+// it computes on the rows that have landed.  x is read XB steps at a time, one batch ahead.
+// `wleaf` is the leaf's first row; rows are `rowbytes` apart (GV_CH * rowbytes < 2^31).
+constexpr int GV_RB = 16;
+constexpr int GV_AHEAD = 3;
+
+template <int BT>
+__device__ __forceinline__ void gv_weights(uint32_t u, const float (&sc)[GvCols<BT>::cpl], float (&wv)[GvCols<BT>::cpl]) {
+  if constexpr (BT == T_F32) {
+    wv[0] = __uint_as_float(u);
+  } else if constexpr (BT == T_BF16) {
+    wv[0] = __uint_as_float(u << 16);
+    wv[1] = __uint_as_float(u & 0xFFFF0000u);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[e] = (float)((int32_t)(u << (24 - 8 * e)) >> 24) * sc[e];
+  }
+}
+
+template <int BT, int MR>
+__device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
+                                             int rowbytes, const float* __restrict__ xl, int64_t k, int m,
+                                             const float (&sc)[GvCols<BT>::cpl]) {
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int NBLK = GV_CH / GV_RB;
+  constexpr int RING = GV_AHEAD + 1;
+  constexpr int XB = MR <= 2 ? 16 : 32 / MR;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, GV_RSRC_WORD3);
+  const float* xr[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) xr[r] = xl + (r < m ? r : m - 1) * k;  // rows past m: never stored
+
+  uint32_t ring[RING][GV_RB];
+#pragma unroll
+  for (int b = 0; b < GV_AHEAD; ++b)
+#pragma unroll
+    for (int i = 0; i < GV_RB; ++i)
+      ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * GV_RB + i) * rowbytes, 0);
+  float xc[MR][XB], xn[MR][XB];
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int q = 0; q < XB; ++q) xc[r][q] = xr[r][q];
+
+#pragma unroll
+  for (int b = 0; b < NBLK; ++b) {
+    if (b + GV_AHEAD < NBLK) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < GV_RB; ++i)
+        ring[(b + GV_AHEAD) % RING][i] =
+            __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ((b + GV_AHEAD) * GV_RB + i) * rowbytes, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q0 = 0; q0 < GV_RB; q0 += XB) {
+      const int s0 = b * GV_RB + q0;
+      if (s0 + XB < GV_CH) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int q = 0; q < XB; ++q) xn[r][q] = xr[r][s0 + XB + q];
       }
 #pragma unroll
-      for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+      for (int q = 0; q < XB; ++q) {
+        float wv[CPL];
+        gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int e = 0; e < CPL; ++e) acc[r][e] = __builtin_fmaf(xc[r][q], wv[e], acc[r][e]);
+      }
+      if (s0 + XB < GV_CH) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int q = 0; q < XB; ++q) xc[r][q] = xn[r][q];
+      }
     }
-    if (it + 1 < items) st.store(wbuf[(it + 1) & 1], xbuf[(it + 1) & 1], tid);
-    __syncthreads();
   }
-  if (pending_cb >= 0) {
-    if (tid == 0) last_flag = pending_prev + 1 == (unsigned int)g.nleaves ? 1u : 0u;
-    __syncthreads();
-    if (last_flag) gv_finish<MR>(g, pending_cb, tid);
+}
+
+template <int BT, int MR, bool VEC, bool FULLLEAF>
+__global__ void __launch_bounds__(GV_THREADS) gemv_nn_kernel(GemvArgs g, const float* __restrict__ x) {
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int COLS = GvCols<BT>::cols;
+  constexpr int EB = Elem<BT>::bytes;
+  __shared__ float part[GV_LEAVES][MR][COLS];
+  __shared__ unsigned int last_flag;
+
+  set_flush_inputs_mode();
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: leaf and k range too
+  const int64_t cg = blockIdx.x % g.ncg;
+  const int64_t grp = blockIdx.x / g.ncg;
+  const int64_t t = grp * GV_LEAVES + wave;  // this wave's leaf
+  const int m = (int)g.m;
+
+  float acc[MR][CPL];
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) acc[r][e] = 0.f;
+
+  if (t < g.nleaves) {
+    // this lane's columns, clamped into the operand (their cells are never stored)
+    int64_t c0 = cg * COLS + lane * CPL;
+    uint32_t coff[CPL];
+    float sc[CPL];
+    if constexpr (VEC) {
+      if (c0 >= g.n) c0 = g.n - CPL;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) coff[e] = (uint32_t)((c0 + e) * EB);
+    } else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) coff[e] = (uint32_t)((c0 + e < g.n ? c0 + e : g.n - 1) * EB);
+    }
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      sc[e] = 1.f;
+      if constexpr (BT == T_I8) sc[e] = g.scales[coff[e]];  // EB == 1: the offset is the column
+    }
+    const char* w = static_cast<const char*>(g.w);
+    const uint32_t loff = coff[0];
+    const int64_t rowbytes = g.n * EB;
+    const int64_t kb = t * g.leaf;
+    const int64_t ke = kb + g.leaf < g.k ? kb + g.leaf : g.k;
+    const int64_t klast = ke - 1;
+
+    if constexpr (FULLLEAF) {
+      gv_leaf_full<BT, MR>(acc, w + kb * rowbytes, loff, (int)rowbytes, x + kb, g.k, m, sc);
+    } else {
+      // The general case: the leaf's rows in pieces of GV_CH (one piece unless the leaf is
+      // longer than 128); every row of a piece is requested before its first step, and the
+      // steps consume them in order as they land.
+      uint32_t buf[GV_CH];
+      for (int64_t p0 = kb; p0 < ke; p0 += GV_CH) {
+        const int64_t nrow = ke - p0;
+        gv_load<BT, VEC>(buf, w, loff, coff, rowbytes, p0, klast);
+        if (nrow >= GV_CH) gv_steps<BT, MR, true>(acc, buf, x, g.k, p0, GV_CH, m, sc);
+        else gv_steps<BT, MR, false>(acc, buf, x, g.k, p0, (int)nrow, m, sc);
+      }
+    }
   }
+
+  // The group's root: the tree over its (up to GV_LEAVES) leaf partials, through LDS.
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) part[wave][r][lane * CPL + e] = acc[r][e];
+  __syncthreads();
+  const int64_t left = g.nleaves - grp * GV_LEAVES;
+  const int cnt = left < GV_LEAVES ? (int)left : GV_LEAVES;
+  for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
+    const int r = cell / COLS, col = cell % COLS;
+    const int64_t j = cg * COLS + col;
+    if (r >= m || j >= g.n) continue;
+    float y = part[0][r][col];
+    if (cnt >= 2) y = y + part[1][r][col];           // leaves 0,1 paired
+    if (cnt == 3) y = y + part[2][r][col];           // leaf 2 carried, then joined
+    if (cnt == 4) y = y + (part[2][r][col] + part[3][r][col]);
+    if (g.ngroups == 1) {
+      if (g.bias) y = y + g.bias[j];  // ftz(C) + ftz(b) by the input flush
+      g.c[r * g.n + j] = store_word(y);
+    } else {
+      __hip_atomic_store(&g.ws[(grp * g.m + r) * g.n + j], y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (g.ngroups == 1) return;
+
+  // Count this group's roots in; the workgroup that completes the count folds.  The roots
+  // are device-coherent stores, complete (vmcnt) before the count is published.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int prev = __hip_atomic_fetch_add(&g.counter[cg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = prev + 1 == (unsigned int)g.ngroups ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  const int64_t stride = g.m * g.n;
+  constexpr int CPT = (MR * COLS + GV_THREADS - 1) / GV_THREADS;  // cells per thread
+  if (g.ngroups <= GV_FEW_GROUPS) {
+    // every root of every cell of this thread requested at once, then folded
+    float v[CPT][GV_FEW_GROUPS];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int cell = tid + c * GV_THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (cell >= MR * COLS || r >= m || j >= g.n) continue;
+#pragma unroll
+      for (int e = 0; e < GV_FEW_GROUPS; ++e)
+        if (e < g.ngroups)
+          v[c][e] = __hip_atomic_load(g.ws + (e * g.m + r) * g.n + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int cell = tid + c * GV_THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (cell >= MR * COLS || r >= m || j >= g.n) continue;
+      StackF stk;
+      const int P = (int)g.ngroups;
+#pragma unroll
+      for (int e = 0; e + 1 < GV_FEW_GROUPS; ++e)
+        if (e + 1 < P) stk.push(v[c][e], e);
+      float y = v[c][0];
+#pragma unroll
+      for (int e = 1; e < GV_FEW_GROUPS; ++e)
+        if (e == P - 1) y = v[c][e];
+      y = stk.root(y, P - 1);
+      if (g.bias) y = y + g.bias[j];
+      g.c[r * g.n + j] = store_word(y);
+    }
+  } else {
+    for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (r >= m || j >= g.n) continue;
+      float y = fold_roots(g.ws + r * g.n + j, g.ngroups, stride);
+      if (g.bias) y = y + g.bias[j];
+      g.c[r * g.n + j] = store_word(y);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&g.counter[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -743,6 +889,9 @@ static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
   while (gsz > 4 && tiles * groups(gsz) < 2 * (int64_t)num_cus) gsz /= 2;
   return (int)gsz;
 }
+
+static int64_t gemv_groups(int64_t P) { return (P + GV_LEAVES - 1) / GV_LEAVES; }
+static int64_t gemv_cols(int bt) { return 64 * (4 / elem_bytes(bt)); }
 
 // The skinny-M path takes OP_NN products with at most GV_MAXM float32 rows.
 static bool use_gemv(const GemmProblem& p) {
@@ -777,7 +926,7 @@ int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus) {
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
   if (P < 1 || p.m <= 0 || p.n <= 0) return 0;
-  if (use_gemv(p)) return P > 1 ? P * p.m * p.n : 0;
+  if (use_gemv(p)) return gemv_groups(P) > 1 ? gemv_groups(P) * p.m * p.n : 0;
   const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
   const int64_t gsz = P > 1 ? pick_group(P, tiles, num_cus) : 1;
   const int64_t ng = (P + gsz - 1) / gsz;
@@ -787,30 +936,33 @@ int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus) {
 int64_t gemm_counter_count(const GemmProblem& p) {
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
-  if (!use_gemv(p) || p.n <= 0 || P <= 1) return 0;
-  return (p.n + GV_COLS - 1) / GV_COLS;
+  if (!use_gemv(p) || p.n <= 0 || gemv_groups(P) <= 1) return 0;
+  return (p.n + gemv_cols(p.b_type) - 1) / gemv_cols(p.b_type);
 }
 
+// vec: 0 element loads, 1 word (buffer) loads, 2 word loads of whole 128-row leaves
 template <int BT, int MR>
-static hipError_t launch_gemv_mr(const GemvArgs& g, bool vec, dim3 grid, hipStream_t s) {
-  if (vec) hipLaunchKernelGGL((gemv_nn_kernel<BT, MR, true>), grid, dim3(GV_THREADS), 0, s, g);
-  else hipLaunchKernelGGL((gemv_nn_kernel<BT, MR, false>), grid, dim3(GV_THREADS), 0, s, g);
+static hipError_t launch_gemv_mr(const GemvArgs& g, const float* x, int vec, dim3 grid, hipStream_t s) {
+  if (vec == 2) hipLaunchKernelGGL((gemv_nn_kernel<BT, MR, true, true>), grid, dim3(GV_THREADS), 0, s, g, x);
+  else if (vec == 1) hipLaunchKernelGGL((gemv_nn_kernel<BT, MR, true, false>), grid, dim3(GV_THREADS), 0, s, g, x);
+  else hipLaunchKernelGGL((gemv_nn_kernel<BT, MR, false, false>), grid, dim3(GV_THREADS), 0, s, g, x);
   return hipGetLastError();
 }
 
 template <int BT>
-static hipError_t launch_gemv_m(const GemvArgs& g, int64_t m, bool vec, dim3 grid, hipStream_t s) {
-  if (m <= 1) return launch_gemv_mr<BT, 1>(g, vec, grid, s);
-  if (m <= 2) return launch_gemv_mr<BT, 2>(g, vec, grid, s);
-  if (m <= 4) return launch_gemv_mr<BT, 4>(g, vec, grid, s);
-  if (m <= 8) return launch_gemv_mr<BT, 8>(g, vec, grid, s);
-  return launch_gemv_mr<BT, 16>(g, vec, grid, s);
+static hipError_t launch_gemv_m(const GemvArgs& g, const float* x, int64_t m, int vec, dim3 grid, hipStream_t s) {
+  if (m <= 1) return launch_gemv_mr<BT, 1>(g, x, vec, grid, s);
+  if (m <= 2) return launch_gemv_mr<BT, 2>(g, x, vec, grid, s);
+  if (m <= 4) return launch_gemv_mr<BT, 4>(g, x, vec, grid, s);
+  if (m <= 8) return launch_gemv_mr<BT, 8>(g, x, vec, grid, s);
+  return launch_gemv_mr<BT, 16>(g, x, vec, grid, s);
 }
 
-static hipError_t launch_gemv_bt(const GemvArgs& g, int bt, int64_t m, bool vec, dim3 grid, hipStream_t s) {
-  if (bt == T_F32) return launch_gemv_m<T_F32>(g, m, vec, grid, s);
-  if (bt == T_BF16) return launch_gemv_m<T_BF16>(g, m, vec, grid, s);
-  return launch_gemv_m<T_I8>(g, m, vec, grid, s);
+static hipError_t launch_gemv_bt(const GemvArgs& g, const float* x, int bt, int64_t m, int vec, dim3 grid,
+                                 hipStream_t s) {
+  if (bt == T_F32) return launch_gemv_m<T_F32>(g, x, m, vec, grid, s);
+  if (bt == T_BF16) return launch_gemv_m<T_BF16>(g, x, m, vec, grid, s);
+  return launch_gemv_m<T_I8>(g, x, m, vec, grid, s);
 }
 
 template <int OP, int AT, int BT>
@@ -844,22 +996,18 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
   }
   if (use_gemv(p)) {
     GemvArgs v;
-    v.c = p.c; v.x = static_cast<const float*>(p.a); v.w = p.b; v.scales = p.scales; v.bias = p.bias;
+    v.c = p.c; v.w = p.b; v.scales = p.scales; v.bias = p.bias;
     v.ws = ws; v.counter = counters;
     v.m = p.m; v.n = p.n; v.k = p.k; v.leaf = L; v.nleaves = P;
-    if (P > 1 && (ws == nullptr || counters == nullptr)) return hipErrorInvalidValue;
+    v.ngroups = gemv_groups(P);
+    v.ncg = (p.n + gemv_cols(p.b_type) - 1) / gemv_cols(p.b_type);
+    if (v.ngroups > 1 && (ws == nullptr || counters == nullptr)) return hipErrorInvalidValue;
     const int eb = elem_bytes(p.b_type);
-    const int rows = GV_CHUNK / (GV_COLS * eb);
-    v.chunks = (int)((L + rows - 1) / rows);
-    v.ncb = (p.n + GV_COLS - 1) / GV_COLS;
-    v.ntasks = v.ncb * P;
-    const bool vec = ((p.n * eb) % 16 == 0) && aligned(p.b, 16);
-    // persistent grid: as many 256-thread workgroups as are resident at once (LDS: 64 KB of W
-    // buffers plus x's two buffers each, two per CU while that fits in 160 KB)
-    const int64_t lds = 2 * (int64_t)GV_CHUNK + 2 * (int64_t)rows * (p.m <= 1 ? 1 : p.m <= 2 ? 2 : p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16) * 4;
-    int64_t grid = (lds * 2 <= 160 * 1024 ? 2 : 1) * (int64_t)num_cus;
-    if (grid > v.ntasks) grid = v.ntasks;
-    return launch_gemv_bt(v, p.b_type, p.m, vec, dim3((unsigned)grid), stream);
+    // word loads need 4-byte rows and base, and GV_CH rows within a 31-bit buffer offset
+    int vec = ((p.n * eb) % 4 == 0) && aligned(p.b, 4) && (int64_t)GV_CH * p.n * eb < (int64_t(1) << 31) ? 1 : 0;
+    if (vec && L == GV_CH && p.k % GV_CH == 0) vec = 2;
+    const int64_t grid = v.ncg * v.ngroups;
+    return launch_gemv_bt(v, static_cast<const float*>(p.a), p.b_type, p.m, vec, dim3((unsigned)grid), stream);
   }
   GemmArgs g;
   g.c = p.c; g.a = p.a; g.b = p.b; g.scales = p.scales; g.bias = p.bias; g.ws = ws;

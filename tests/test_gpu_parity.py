@@ -201,14 +201,16 @@ def test_bf16_conversions(oracle):
 
 
 GEMV_SHAPES = [(1, 1, 1), (1, 255, 129), (2, 256, 128), (7, 257, 1000), (16, 1000, 4096), (1, 4100, 300),
-               (3, 4096, 4097), (16, 33, 2048), (1, 14336, 4096)]
+               (3, 4096, 4097), (16, 33, 2048), (1, 14336, 4096), (2, 70, 140000), (5, 300, 515)]
 
 
 @pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
 @pytest.mark.parametrize("shape", GEMV_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_SHAPES])
 def test_skinny_m(oracle, shape, wt):
-    """The skinny-M (decode GEMV) path: LDS-staged W blocks, pair-of-leaves workgroups and the
-    last-arriver fold across workgroups; 16-byte and element-wise staging."""
+    """The skinny-M (decode GEMV) path: a leaf per wave streamed into registers (word loads,
+    or element loads when a row is not a multiple of 4 bytes), groups of 4 leaves folded in
+    LDS, the last-arriving group folding the rest; leaves longer than 128 rows (k > 131072),
+    ragged last leaves, ragged last groups."""
     D = _dev()
     m, n, k = shape
     rng = np.random.default_rng(m + n + k)
