@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+
 #include "contract.h"
 #include "kernels.h"
 
@@ -53,7 +54,7 @@ __device__ __forceinline__ float store_word(float x) {
 // Tiling: 512 threads = 8 waves (2 per SIMD); workgroup tile 128 x 128 cells; each
 // wave owns 64 rows x 32 columns = one v_mfma_f32_32x32x1_2b_f32 per k step (block 0 =
 // rows 0-31, block 1 = rows 32-63, both against the same 32 columns).  K is staged
-// through LDS in KT = 32-step slices, double buffered.  Operands travel global -> LDS
+// through LDS in KT = 32-step slices, three buffers (loads issued two slices ahead).  Operands travel global -> LDS
 // with global_load_lds_dwordx4 (16 bytes per lane, straight into LDS, no registers) in
 // their stored element type; bf16 widening and int8 x column-scale dequantisation
 // happen when a lane reads its MFMA operand out of LDS.
@@ -63,6 +64,7 @@ constexpr int BM = 128;
 constexpr int BN = 128;
 constexpr int KT = 32;
 constexpr int SLICE_BYTES = BM * KT * 4;  // one operand slice at float32: 16 KB
+constexpr int NBUF = 3;                   // slices in LDS: loads run two slices ahead
 constexpr int MAX_GROUP_LEAVES = 32;      // one group's leaves fold in registers + one LDS slot
 
 typedef __attribute__((address_space(3))) void* lds_vptr;
@@ -107,57 +109,68 @@ struct Slice {
   }
 };
 
-// The global side of one operand: this lane's share of every slice's load instructions.
-// `pitch` is the stored row length in elements (a multiple of 16 bytes; the base is
-// 16-byte aligned), `nidx` the operand's index count (m or n) and `krows` = k.  A chunk
-// outside the operand is read from an in-bounds chunk instead: an index past the end
-// reads the last index (its cells are never stored), a step past k reads the last stored
-// chunk (no chain step reads it), so every load is in bounds and none is predicated.
+// Word 3 of a raw buffer resource on gfx9-family targets (32-bit data format, no swizzle).
+constexpr int RSRC_WORD3 = 0x00020000;
+
+// The global side of one operand: this lane's share of every slice's load instructions, as
+// buffer loads straight into LDS.  Load instruction q of a slice covers RPI consecutive
+// stored rows; its scalar resource starts at the first of them and ends at the operand's
+// end, and the lane's byte offset within it is fixed for the whole k loop.  A chunk past
+// the operand's end reads as zeros (the resource's record bound); a chunk past a row's
+// end reads the next row's bytes.  Neither reaches a stored cell: indices past m or n are
+// never stored, steps past k are never executed.  The host keeps RPI * pitch * bytes
+// below 2^31.
 template <int T, bool IMAJ>
 struct DirectLoader {
   using S = Slice<T, IMAJ>;
-  const char* ptr[S::PER_WAVE];  // this lane's chunk with its step offset removed
-  int dk[S::PER_WAVE];
+  static constexpr int RPI = IMAJ ? 64 / S::CR : 64 / S::RC;  // stored rows per instruction
+  uint32_t voff[S::PER_WAVE];
 
-  __device__ __forceinline__ void init(const void* base, int64_t nidx, int64_t pitch, int64_t idx0,
-                                       int wave, int lane) {
+  __device__ __forceinline__ void init(int64_t pitch, int wave, int lane) {
 #pragma unroll
     for (int h = 0; h < S::PER_WAVE; ++h) {
-      const int q = wave + NWAVES * h;
-      int di, d;
-      S::coords((q < S::NI ? q : 0) * 64 + lane, di, d);
-      int64_t i = idx0 + di;
-      if constexpr (IMAJ) {
-        if (i >= nidx) i = nidx - 1;
-        ptr[h] = static_cast<const char*>(base) + i * pitch * S::EB;
-      } else {
-        if (i + S::CE > pitch) i = pitch - S::CE;
-        ptr[h] = static_cast<const char*>(base) + i * S::EB;
-      }
-      dk[h] = d;
+      const int q = (wave + NWAVES * h) % S::NI;
+      int di, dk;
+      S::coords(q * 64 + lane, di, dk);
+      if constexpr (IMAJ) voff[h] = (uint32_t)(((di - q * RPI) * pitch + dk) * S::EB);
+      else voff[h] = (uint32_t)(((dk - q * RPI) * pitch + di) * S::EB);
     }
   }
 
-  // Issue this wave's loads of the slice that starts at step k0 into `slice`.
-  __device__ __forceinline__ void issue(char* slice, int64_t k0, int64_t pitch, int64_t krows,
-                                        int wave) const {
+  // Issue this wave's PER_WAVE loads of the slice that starts at step k0 into `slice` (when
+  // a slice has fewer load instructions than waves, the extra waves repeat an earlier
+  // wave's chunk -- the same bytes to the same place -- so every wave issues the same
+  // count and can wait on it with one vmcnt).  `wave` must be wave-uniform.
+  __device__ __forceinline__ void issue(char* slice, const void* base, int64_t total_bytes, int64_t pitch,
+                                        int64_t idx0, int64_t k0, int wave) const {
 #pragma unroll
     for (int h = 0; h < S::PER_WAVE; ++h) {
-      const int q = wave + NWAVES * h;
-      if (S::NI % NWAVES != 0 && q >= S::NI) break;  // wave-uniform
-      int64_t kk = k0 + dk[h];
-      const char* src;
-      if constexpr (IMAJ) {
-        if (kk + S::CE > pitch) kk = pitch - S::CE;
-        src = ptr[h] + kk * S::EB;
-      } else {
-        if (kk >= krows) kk = krows - 1;
-        src = ptr[h] + kk * pitch * S::EB;
-      }
-      __builtin_amdgcn_global_load_lds((gbl_vptr)src, (lds_vptr)(slice + q * 1024), 16, 0, 0);
+      const int q = (wave + NWAVES * h) % S::NI;
+      const int64_t off = IMAJ ? ((idx0 + q * RPI) * pitch + k0) * S::EB : ((k0 + q * RPI) * pitch + idx0) * S::EB;
+      const int64_t rem = total_bytes - off;
+      const int nrec = rem <= 0 ? 0 : (rem > 0x7FFFFFFF ? 0x7FFFFFFF : (int)rem);
+      const char* first = static_cast<const char*>(base) + (rem > 0 ? off : 0);
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(first), (short)0, nrec, RSRC_WORD3);
+#if defined(__HIP_DEVICE_COMPILE__)
+      // (the host pass compiles kernel bodies only for their launch stubs; with this builtin
+      // in a kernel template it drops the stubs of every instantiation after the first)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_vptr)(slice + q * 1024), 16, voff[h], 0, 0, 0);
+#else
+      (void)rs;
+#endif
     }
   }
 };
+
+// A workgroup barrier for LDS hand-off only: no wait on this wave's outstanding global
+// loads (the k loop waits for exactly the slice it needs), a compiler fence on each side.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 // A lane's MFMA operand values for steps s .. s+3 of a staged slice, as float32: index
 // `idx` of the slice.  bf16 widens exactly (bits << 16); int8 is f32(code) * scale, one
@@ -263,6 +276,7 @@ struct GemmArgs {
   int64_t group;      // leaves per group (power of two, <= 32)
   int64_t ngroups;
   int64_t a_pitch, b_pitch;  // stored row lengths in elements
+  int64_t a_bytes, b_bytes;  // stored operand sizes
   int tiles_n;
 };
 
@@ -298,14 +312,18 @@ template <int OP, int AT, int BT>
 __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   constexpr bool A_IMAJ = (OP != OP_TN);
   constexpr bool B_IMAJ = (OP == OP_NT);
-  __shared__ __attribute__((aligned(1024))) char lds[2][2][SLICE_BYTES];  // [buffer][A,B]
+  // three slice buffers [A, B], separate objects so the compiler can tell them apart
+  __shared__ __attribute__((aligned(1024))) char lds0[2][SLICE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds1[2][SLICE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds2[2][SLICE_BYTES];
+
   __shared__ f4 slot4[NWAVES][8][64];  // fold slot 4, per wave
 
   set_flush_inputs_mode();
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 2;  // 0..1: rows wr*64 .. +63
   const int wc = wave & 3;   // 0..3: cols wc*32 .. +31
 
@@ -327,10 +345,18 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
 
   DirectLoader<AT, A_IMAJ> lda;
   DirectLoader<BT, B_IMAJ> ldb;
-  lda.init(g.a, g.m, g.a_pitch, i0, wave, lane);
-  ldb.init(g.b, g.n, g.b_pitch, j0, wave, lane);
-  lda.issue(lds[0][0], kt_first * KT, g.a_pitch, g.k, wave);
-  ldb.issue(lds[0][1], kt_first * KT, g.b_pitch, g.k, wave);
+  lda.init(g.a_pitch, wave, lane);
+  ldb.init(g.b_pitch, wave, lane);
+  // loads per slice per wave: every wave issues the same count, so vmcnt(LPS) waits for all
+  // but the most recent slice's loads
+  constexpr int LPS = Slice<AT, A_IMAJ>::PER_WAVE + Slice<BT, B_IMAJ>::PER_WAVE;
+  constexpr int WAIT_ONE_BEHIND = (LPS & 0xF) | ((LPS >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+  // Slices are loaded unconditionally, two ahead: one past the group's last slice reads
+  // zeros or bytes no step uses (the resource bounds keep it inside the operand).
+  lda.issue(lds0[0], g.a, g.a_bytes, g.a_pitch, i0, kt_first * KT, wave);
+  ldb.issue(lds0[1], g.b, g.b_bytes, g.b_pitch, j0, kt_first * KT, wave);
+  lda.issue(lds1[0], g.a, g.a_bytes, g.a_pitch, i0, (kt_first + 1) * KT, wave);
+  ldb.issue(lds1[1], g.b, g.b_bytes, g.b_pitch, j0, (kt_first + 1) * KT, wave);
 
   const int arow = wr * 64 + lane;
   const int bcol = wc * 32 + (lane & 31);
@@ -351,46 +377,59 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   int64_t leaf_end = (t_first + 1) * g.leaf;
   if (leaf_end > g.k) leaf_end = g.k;
 
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's slice loads have landed
-  __syncthreads();
+  // the first slice has landed (the second may still be in flight)
+  __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND);
+  lds_barrier();
 
-  int buf = 0;
-  for (int64_t kt = kt_first; kt <= kt_last; ++kt) {
-    if (kt < kt_last) {
-      // The other buffer was last read before the barrier that ended the previous slice.
-      lda.issue(lds[buf ^ 1][0], (kt + 1) * KT, g.a_pitch, g.k, wave);
-      ldb.issue(lds[buf ^ 1][1], (kt + 1) * KT, g.b_pitch, g.k, wave);
-    }
-    const char* la = lds[buf][0];
-    const char* lb = lds[buf][1];
-    const int64_t tbase = kt * KT;
-    int64_t pos = tbase > kb ? tbase : kb;
-    int64_t hi = tbase + KT;
-    if (hi > ke) hi = ke;
-    while (pos < hi) {
-      const int64_t seg = hi < leaf_end ? hi : leaf_end;
-      if (pos == tbase && seg == tbase + KT)
-        mfma_steps<OP, AT, BT, true>(acc, la, lb, 0, KT, arow, bcol, scale);
-      else
-        mfma_steps<OP, AT, BT, false>(acc, la, lb, (int)(pos - tbase), (int)(seg - tbase), arow, bcol, scale);
-      pos = seg;
-      if (pos == leaf_end) {
-        if (t + 1 < cnt) {
-          stk.push(acc, t);
-#pragma unroll
-          for (int e = 0; e < 32; ++e) acc[e] = 0.f;
-          ++t;
-          leaf_end = (t_first + t + 1) * g.leaf;
-          if (leaf_end > g.k) leaf_end = g.k;
-        } else {
-          acc = stk.root(acc, t);  // the group's root; no step follows the last leaf
-        }
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next slice's loads have landed
-    __syncthreads();
-    buf ^= 1;
+  // One slice: fill buffer FILL with slice kt + 2 (it was last read before the previous
+  // slice's barrier), run slice kt's steps out of buffer CUR (pushing each finished leaf;
+  // after the group's last leaf acc holds the group's root), wait for slice kt + 1.  The
+  // loop below is unrolled by NBUF, so every step names its buffers as distinct objects and
+  // the compiler does not make the reads of slice kt wait for the loads of slice kt + 2.
+#define MLG_SLICE_STEP(CUR, FILL) \
+  do { \
+    lda.issue(FILL[0], g.a, g.a_bytes, g.a_pitch, i0, (kt + 2) * KT, wave); \
+    ldb.issue(FILL[1], g.b, g.b_bytes, g.b_pitch, j0, (kt + 2) * KT, wave); \
+    const char* la = CUR[0]; \
+    const char* lb = CUR[1]; \
+    const int64_t tbase = kt * KT; \
+    int64_t pos = tbase > kb ? tbase : kb; \
+    int64_t hi = tbase + KT; \
+    if (hi > ke) hi = ke; \
+    while (pos < hi) { \
+      const int64_t seg = hi < leaf_end ? hi : leaf_end; \
+      if (pos == tbase && seg == tbase + KT) \
+        mfma_steps<OP, AT, BT, true>(acc, la, lb, 0, KT, arow, bcol, scale); \
+      else \
+        mfma_steps<OP, AT, BT, false>(acc, la, lb, (int)(pos - tbase), (int)(seg - tbase), arow, bcol, scale); \
+      pos = seg; \
+      if (pos == leaf_end) { \
+        if (t + 1 < cnt) { \
+          stk.push(acc, t); \
+          _Pragma("unroll") for (int e = 0; e < 32; ++e) acc[e] = 0.f; \
+          ++t; \
+          leaf_end = (t_first + t + 1) * g.leaf; \
+          if (leaf_end > g.k) leaf_end = g.k; \
+        } else { \
+          acc = stk.root(acc, t); \
+        } \
+      } \
+    } \
+    __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND); \
+    lds_barrier(); \
+  } while (0)
+  static_assert(NBUF == 3, "the slice loop is unrolled by NBUF");
+  for (int64_t kt = kt_first; kt <= kt_last;) {
+    MLG_SLICE_STEP(lds0, lds2);
+    if (++kt > kt_last) break;
+    MLG_SLICE_STEP(lds1, lds0);
+    if (++kt > kt_last) break;
+    MLG_SLICE_STEP(lds2, lds1);
+    ++kt;
   }
+#undef MLG_SLICE_STEP
+  // no load into LDS may outlive the workgroup
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
   // acc holds the group root.  Element e -> block b = e/16, row (e%4) + 8*((e%16)/4) + 4*(lane/32) within it.
   const int64_t col = j0 + bcol;
@@ -539,9 +578,6 @@ __device__ __forceinline__ float fold_roots(const float* base, int64_t P, int64_
   return stk.root(last, (int)t);
 }
 
-// Word 3 of a raw buffer resource on gfx9-family targets (32-bit data format, no swizzle).
-constexpr int GV_RSRC_WORD3 = 0x00020000;
-
 // Load the words of rows k0 .. k0+GV_CH-1 (rows past `klast` read row `klast`: in bounds,
 // and no chain step uses them).  VEC: buffer loads, the chunk's first row in a scalar
 // resource, the row offset i*rowbytes in the scalar offset and the lane's byte offset
@@ -553,7 +589,7 @@ __device__ __forceinline__ void gv_load(uint32_t (&buf)[GV_CH], const char* w, u
   const int64_t last = klast - k0;  // >= GV_CH - 1 for a full chunk
   if constexpr (VEC) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(w + k0 * rowbytes), (short)0, 0x7FFFFFFF, GV_RSRC_WORD3);
+        const_cast<char*>(w + k0 * rowbytes), (short)0, 0x7FFFFFFF, RSRC_WORD3);
 #pragma unroll
     for (int i = 0; i < GV_CH; ++i) {
       const int ii = i <= last ? i : (int)last;
@@ -671,7 +707,7 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], 
   constexpr int RING = GV_AHEAD + 1;
   constexpr int XB = MR <= 2 ? 16 : 32 / MR;
   const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, GV_RSRC_WORD3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
   const float* xr[MR];
 #pragma unroll
   for (int r = 0; r < MR; ++r) xr[r] = xl + (r < m ? r : m - 1) * k;  // rows past m: never stored
@@ -1038,7 +1074,10 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
       src = wsp;
       wsp += is_a ? ra : rb;
     }
-    if (is_a) { g.a = src; g.a_pitch = pitch; } else { g.b = src; g.b_pitch = pitch; }
+    if (is_a) { g.a = src; g.a_pitch = pitch; g.a_bytes = rows * pitch * eb; }
+    else { g.b = src; g.b_pitch = pitch; g.b_bytes = rows * pitch * eb; }
+    // one load instruction spans at most 32 stored rows (int8, index-major)
+    if ((32 * pitch + KT) * eb >= (int64_t(1) << 31)) return hipErrorInvalidValue;
   }
   dim3 grid((unsigned)(tm * tn), (unsigned)g.ngroups);
   hipError_t e;
