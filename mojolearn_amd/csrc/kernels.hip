@@ -918,11 +918,11 @@ static int elem_bytes(int t) { return t == T_F32 ? 4 : (t == T_BF16 ? 2 : 1); }
 
 static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
   // Largest power-of-two group <= 32 leaves; split further (aligned subtrees) while the
-  // grid is smaller than two workgroups per CU and groups still hold >= 4 leaves.
+  // grid has fewer workgroups than CUs (one 160 KB workgroup fits a CU).
   int64_t gsz = 32;
   while (gsz > 1 && gsz / 2 >= nleaves) gsz /= 2;
   auto groups = [&](int64_t s) { return (nleaves + s - 1) / s; };
-  while (gsz > 4 && tiles * groups(gsz) < 2 * (int64_t)num_cus) gsz /= 2;
+  while (gsz > 1 && tiles * groups(gsz) < (int64_t)num_cus) gsz /= 2;
   return (int)gsz;
 }
 
