@@ -164,6 +164,45 @@ def cpu_baseline(W, O, min_seconds=10.0, max_seconds=30.0):
                       f"oracle/gemm_oracle.c fast arm (AVX2 FMA), {threads} threads, {dt:.1f} s"}
 
 
+def bench_compare(torch, D, steps, warmup):
+    """The rows the reference publishes for this path on MI325X (its own results tree), measured
+    the same way here: fp32.v1 512x4096x4096 OP_NT, fp32-weight GEMV 1x14336x4096 (OP_NN and the
+    LM layout OP_NT, 235 MB of weights, 4 rotating copies), and the host-pointer surface
+    `linalg.matmul` on 4096^3 numpy arrays (upload, product, download, NaN canon), median of 5."""
+    from mojolearn_amd import linalg
+    rng = np.random.default_rng(7)
+    out = {}
+    a = rng.standard_normal((512, 4096), dtype=np.float32)
+    w = rng.standard_normal((4096, 4096), dtype=np.float32)
+    plan = D.Plan(_t(torch, a), _t(torch, w), op=D.OP_NT)
+    ms = graph_time([plan], steps, warmup, torch)
+    out["nt_512x4096x4096"] = {"ms": ms, "tflops": 2.0 * 512 * 4096 * 4096 / (ms * 1e-3) / 1e12,
+                               "reference_mi325x_tflops": 18.6}
+    x = rng.standard_normal((1, 4096), dtype=np.float32)
+    for name, op, shape in (("gemv_f32_nn_1x14336x4096", D.OP_NN, (4096, 14336)),
+                            ("gemv_f32_nt_1x14336x4096", D.OP_NT, (14336, 4096))):
+        tx = _t(torch, x)
+        ws = [torch.randn(shape, dtype=torch.float32, device="cuda:0") for _ in range(4)]
+        o = torch.empty((1, 14336), dtype=torch.float32, device="cuda:0")
+        plans = [D.Plan(tx, wi, op=op, out=o) for wi in ws]
+        ms = graph_time(plans, max(steps, 8), warmup, torch)
+        nbytes = 4 * (4096 * 14336 + 4096 + 14336)
+        out[name] = {"ms": ms, "us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9, "reference_mi325x_gbs": 1440.0}
+        del plans, ws
+    ha = rng.standard_normal((4096, 4096), dtype=np.float32)
+    hb = rng.standard_normal((4096, 4096), dtype=np.float32)
+    linalg.matmul(ha, hb)
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        linalg.matmul(ha, hb)
+        times.append((time.perf_counter() - t0) * 1e3)
+    times.sort()
+    out["host_matmul_4096"] = {"ms": times[2], "tflops": 2.0 * 4096 ** 3 / (times[2] * 1e-3) / 1e12,
+                               "reference_mi325x_ms": 28.2}
+    return out
+
+
 def copy_calibration(torch, nbytes=1 << 30):
     """Three copies of a 1 GiB float32 buffer (torch's elementwise copy kernel): each dispatch
     reads and writes exactly `nbytes`, the yardstick for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -184,6 +223,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-check", action="store_true", help="skip the oracle comparison")
     ap.add_argument("--eager", action="store_true", help="time eager launches, no HIP graph")
+    ap.add_argument("--compare", action="store_true",
+                    help="also measure the rows the reference publishes for this path (MI325X)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (the byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -223,6 +264,9 @@ def main():
             torch, D, x, w, max(3, args.steps // 2), 1,
             want_fn=(lambda r: O.nan_canon(O.gemm_fast(x[r], w, 0))) if check else None)
 
+    if args.compare:
+        extra["compare"] = bench_compare(torch, D, args.steps, args.warmup)
+
     line = {
         "metric": "identical-mode FP32 GEMM TFLOP/s & % of peak; GEMV GB/s; 0 mismatched bits",
         "value": round(pre["tflops"], 3),
@@ -247,9 +291,13 @@ def main():
     if check:
         line["mismatched_words"] = pre["mismatched_words"]
         line["checked_cells"] = pre["checked_cells"]
+    def _round(v):
+        if isinstance(v, dict):
+            return {kk: _round(vv) for kk, vv in v.items()}
+        return round(v, 4) if isinstance(v, float) else v
+
     if extra:
-        line["workloads"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                             for k, v in extra.items()}
+        line["workloads"] = _round(extra)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(W, O)
     print(json.dumps(line), flush=True)

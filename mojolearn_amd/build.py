@@ -1,7 +1,14 @@
-"""Build libmlgemm.so in place with hipcc for gfx950 (no GPU needed to compile)."""
+"""Build libmlgemm.so in place with hipcc for gfx950 (no GPU needed to compile).
+
+Each translation unit is compiled to an object in a temporary directory, the units in
+parallel (the skinny-M kernels instantiate many template variants and dominate the time),
+then linked into mojolearn_amd/libmlgemm.so.
+"""
 import os
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -13,24 +20,37 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     # packed fp32 (v_pk_fma_f32 and friends) stays off in every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["kernels.hip", "capi.hip"]
+SOURCES = ["gemv_nn.hip", "gemv_nt.hip", "gemm_mfma.hip", "kernels.hip", "capi.hip"]
 
 
-def build(verbose=False, extra=()):
-    cmd = [HIPCC, *FLAGS, *extra, *[os.path.join(CSRC, s) for s in SOURCES], "-o", LIB + ".tmp"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
-    if r.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + err)
-    if err.strip() and verbose:
-        print(err, file=sys.stderr)
+def _clean(stderr):
+    return "\n".join(l for l in stderr.splitlines() if "packed-fp32-ops" not in l)
+
+
+def build(verbose=False, extra=(), jobs=None):
+    with tempfile.TemporaryDirectory(prefix="mlgemm_build_") as tmp:
+        objs = [os.path.join(tmp, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        cmds = [[HIPCC, *FLAGS, *extra, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+        if verbose:
+            for c in cmds:
+                print(" ".join(c), flush=True)
+        with ThreadPoolExecutor(max_workers=jobs or len(cmds)) as pool:
+            results = list(pool.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds))
+        for c, r in zip(cmds, results):
+            if r.returncode != 0:
+                raise RuntimeError(f"hipcc failed on {c[-3]}:\n" + _clean(r.stderr))
+            if verbose and _clean(r.stderr).strip():
+                print(_clean(r.stderr), file=sys.stderr)
+        link = [HIPCC, "--offload-arch=gfx950", "-fPIC", "-shared", *objs, "-o", LIB + ".tmp"]
+        if verbose:
+            print(" ".join(link), flush=True)
+        r = subprocess.run(link, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError("hipcc link failed:\n" + _clean(r.stderr))
     os.replace(LIB + ".tmp", LIB)
     return LIB
 

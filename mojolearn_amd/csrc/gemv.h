@@ -1,0 +1,54 @@
+// The skinny-M (decode GEMV) kernels (gemv_nn.hip, gemv_nt.hip): constants, argument block, launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlg {
+
+// Skinny-M product (decode GEMV), OP_NN: X[M x K] . W[K x N], M <= 16.
+//
+// A wave owns one k-leaf of one column group.  Each lane owns CPL = 4 / bytes consecutive
+// columns: one 32-bit word of W per k row (4 int8 codes, 2 bf16 or 1 float32), so the 64
+// lanes read 256 contiguous bytes of every W row.  The leaf's rows stream into registers
+// GV_CH at a time, two buffers requested before the first arithmetic (a whole 128-row leaf
+// is in flight at once), and each lane runs CPL x M serial chains in VALU (v_fma_f32 under
+// MODE.FP_DENORM = 2 is fma(ftz a, ftz b, ftz acc), like the K=1 MFMA).  x is the same for
+// every lane and is read with uniform loads.  A 256-thread workgroup is one column group's
+// aligned group of GV_LEAVES leaves -- a subtree of the fold -- whose root it forms through
+// LDS.  With more than one group, the roots go to the workspace with agent-scope atomic
+// stores and are counted on the column group's counter; the workgroup that completes the
+// count folds them (the rest of the contract's tree), writes the output and resets the
+// counter.  One launch computes the whole product.
+constexpr int GV_THREADS = 256;
+constexpr int GV_LEAVES = GV_THREADS / 64;  // leaves per workgroup: an aligned subtree
+constexpr int GV_MAXM = 16;
+constexpr int GV_CH = 128;                  // W rows per register buffer: a whole contract leaf
+constexpr int GV_FOLD_BATCH = 32;           // root loads in flight while folding
+constexpr int GV_FEW_GROUPS = 8;            // up to this many groups: all roots loaded at once
+
+template <int T, bool NT = false>
+struct GvCols {
+  static constexpr int cpl = NT ? 1 : 4 / Elem<T>::bytes;  // columns per lane
+  static constexpr int cols = 64 * cpl;                    // columns per group
+};
+
+struct GemvArgs {
+  float* c;
+  const void* w;
+  const float* scales;
+  const float* bias;
+  float* ws;              // [ngroups][m][n] group roots when ngroups > 1
+  unsigned int* counter;  // [ncg], zero between launches (ngroups > 1)
+  int64_t m, n, k, leaf, nleaves;
+  int64_t ngroups;        // ceil(nleaves / GV_LEAVES)
+  int64_t ncg;            // column groups
+};
+
+// vec (OP_NN): 0 element loads, 1 word (buffer) loads, 2 word loads of whole 128-row leaves.
+hipError_t launch_gemv_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,
+                          hipStream_t stream);
+// vec (OP_NT): 0 element loads, 1 16-byte loads.
+hipError_t launch_gemv_nt(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,
+                          hipStream_t stream);
+
+}  // namespace mlg

@@ -1,0 +1,451 @@
+// Device body of the skinny-M kernels, shared by gemv_nn.hip and gemv_nt.hip.
+#pragma once
+#include "device_common.h"
+#include "gemv.h"
+
+namespace mlg {
+
+// The contract's tree over a cell's P roots base[t * stride], read with agent-scope atomic
+// loads issued up to GV_FOLD_BATCH at a time.
+__device__ __forceinline__ float fold_roots(const float* base, int64_t P, int64_t stride) {
+  StackF stk;
+  int64_t t = 0;
+  float last = 0.f;
+  for (int64_t t0 = 0; t0 < P; t0 += GV_FOLD_BATCH) {
+    float v[GV_FOLD_BATCH];
+#pragma unroll
+    for (int e = 0; e < GV_FOLD_BATCH; ++e)
+      if (t0 + e < P) v[e] = __hip_atomic_load(base + (t0 + e) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int e = 0; e < GV_FOLD_BATCH; ++e) {
+      if (t0 + e >= P) break;
+      t = t0 + e;
+      if (t + 1 < P) stk.push(v[e], (int)t);
+      else last = v[e];
+    }
+  }
+  return stk.root(last, (int)t);
+}
+
+// Load the words of rows k0 .. k0+GV_CH-1 (rows past `klast` read row `klast`: in bounds,
+// and no chain step uses them).  VEC: buffer loads, the chunk's first row in a scalar
+// resource, the row offset i*rowbytes in the scalar offset and the lane's byte offset
+// `loff` in one VGPR (the host keeps GV_CH * rowbytes below 2^31).  Otherwise one load per
+// element at the per-column offsets `coff`.
+template <int BT, bool VEC>
+__device__ __forceinline__ void gv_load(uint32_t (&buf)[GV_CH], const char* w, uint32_t loff, const uint32_t* coff,
+                                        int64_t rowbytes, int64_t k0, int64_t klast) {
+  const int64_t last = klast - k0;  // >= GV_CH - 1 for a full chunk
+  if constexpr (VEC) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(w + k0 * rowbytes), (short)0, 0x7FFFFFFF, RSRC_WORD3);
+#pragma unroll
+    for (int i = 0; i < GV_CH; ++i) {
+      const int ii = i <= last ? i : (int)last;
+      buf[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ii * (int)rowbytes, 0);
+    }
+  } else {
+    constexpr int CPL = GvCols<BT>::cpl;
+#pragma unroll
+    for (int i = 0; i < GV_CH; ++i) {
+      const int64_t ii = i <= last ? i : last;
+      const char* row = w + (k0 + ii) * rowbytes;
+      uint32_t u = 0;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        if constexpr (BT == T_F32) u = *reinterpret_cast<const uint32_t*>(row + coff[e]);
+        else if constexpr (BT == T_BF16) u |= (uint32_t)*reinterpret_cast<const uint16_t*>(row + coff[e]) << (16 * e);
+        else u |= (uint32_t)*reinterpret_cast<const uint8_t*>(row + coff[e]) << (8 * e);
+      }
+      buf[i] = u;
+    }
+  }
+}
+
+// x values for steps k0+i0 .. k0+i0+XB-1 of every row (uniform loads; a row past m reads
+// row m-1 and a step past k reads step k-1 -- in bounds, and no chain step uses them).
+template <int MR, int XB, bool FULL>
+__device__ __forceinline__ void gv_load_x(float (&xv)[MR][XB], const float* __restrict__ x, int64_t k, int64_t k0,
+                                          int i0, int m) {
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    const float* xr = x + (r < m ? r : m - 1) * k;
+#pragma unroll
+    for (int q = 0; q < XB; ++q) {
+      if constexpr (FULL) {
+        xv[r][q] = xr[k0 + i0 + q];  // a full chunk lies inside the leaf
+      } else {
+        const int64_t kk = k0 + i0 + q < k ? k0 + i0 + q : k - 1;
+        xv[r][q] = xr[kk];
+      }
+    }
+  }
+}
+
+// Chain steps for rows k0 .. k0+nrows-1 (all GV_CH when FULL).  W[p, j] as float32: bf16
+// widened exactly; int8 f32(code) * scale[j], one rounding (the scale flushed on input).
+// x is read XB steps at a time, one batch ahead.
+template <int BT, int MR, bool FULL>
+__device__ __forceinline__ void gv_steps(float (&acc)[MR][GvCols<BT>::cpl], const uint32_t (&buf)[GV_CH],
+                                         const float* __restrict__ x, int64_t k, int64_t k0, int nrows,
+                                         int m, const float (&sc)[GvCols<BT>::cpl]) {
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int XB = MR >= 16 ? 1 : 16 / MR;
+  float xc[MR][XB], xn[MR][XB];
+  gv_load_x<MR, XB, FULL>(xc, x, k, k0, 0, m);
+#pragma unroll
+  for (int b = 0; b < GV_CH / XB; ++b) {
+    if (b + 1 < GV_CH / XB) gv_load_x<MR, XB, FULL>(xn, x, k, k0, (b + 1) * XB, m);
+#pragma unroll
+    for (int q = 0; q < XB; ++q) {
+      const int i = b * XB + q;
+      if (!FULL && i >= nrows) continue;  // uniform
+      const uint32_t u = buf[i];
+      float wv[CPL];
+      if constexpr (BT == T_F32) {
+        wv[0] = __uint_as_float(u);
+      } else if constexpr (BT == T_BF16) {
+        wv[0] = __uint_as_float(u << 16);
+        wv[1] = __uint_as_float(u & 0xFFFF0000u);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv[e] = (float)((int32_t)(u << (24 - 8 * e)) >> 24) * sc[e];
+      }
+      // rows past m (MR rounds m up) run on row m-1's x and are never stored
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) acc[r][e] = __builtin_fmaf(xc[r][q], wv[e], acc[r][e]);
+    }
+    if (b + 1 < GV_CH / XB) {
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int q = 0; q < XB; ++q) xc[r][q] = xn[r][q];
+    }
+  }
+}
+
+// One whole 128-row leaf (the decode shapes: L = 128, k a multiple of 128), straight-line:
+// the rows travel in blocks of GV_RB through a ring of GV_AHEAD + 1 register blocks, GV_AHEAD
+// blocks requested ahead of the one being consumed, so the wave keeps loads in flight while
+// it computes on the rows that have landed.  x is read XB steps at a time, one batch ahead.
+// `wleaf` is the leaf's first row; rows are `rowbytes` apart (GV_CH * rowbytes < 2^31).
+constexpr int GV_RB = 16;
+constexpr int GV_AHEAD = 3;
+
+template <int BT>
+__device__ __forceinline__ void gv_weights(uint32_t u, const float (&sc)[GvCols<BT>::cpl], float (&wv)[GvCols<BT>::cpl]) {
+  if constexpr (BT == T_F32) {
+    wv[0] = __uint_as_float(u);
+  } else if constexpr (BT == T_BF16) {
+    wv[0] = __uint_as_float(u << 16);
+    wv[1] = __uint_as_float(u & 0xFFFF0000u);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[e] = (float)((int32_t)(u << (24 - 8 * e)) >> 24) * sc[e];
+  }
+}
+
+template <int BT, int MR>
+__device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
+                                             int rowbytes, const float* __restrict__ xl, int64_t k, int m,
+                                             const float (&sc)[GvCols<BT>::cpl]) {
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int NBLK = GV_CH / GV_RB;
+  constexpr int RING = GV_AHEAD + 1;
+  constexpr int XB = MR <= 2 ? 16 : 32 / MR;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
+  const float* xr[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) xr[r] = xl + (r < m ? r : m - 1) * k;  // rows past m: never stored
+
+  uint32_t ring[RING][GV_RB];
+#pragma unroll
+  for (int b = 0; b < GV_AHEAD; ++b)
+#pragma unroll
+    for (int i = 0; i < GV_RB; ++i)
+      ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * GV_RB + i) * rowbytes, 0);
+  float xc[MR][XB], xn[MR][XB];
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int q = 0; q < XB; ++q) xc[r][q] = xr[r][q];
+
+#pragma unroll
+  for (int b = 0; b < NBLK; ++b) {
+    if (b + GV_AHEAD < NBLK) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < GV_RB; ++i)
+        ring[(b + GV_AHEAD) % RING][i] =
+            __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ((b + GV_AHEAD) * GV_RB + i) * rowbytes, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q0 = 0; q0 < GV_RB; q0 += XB) {
+      const int s0 = b * GV_RB + q0;
+      if (s0 + XB < GV_CH) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int q = 0; q < XB; ++q) xn[r][q] = xr[r][s0 + XB + q];
+      }
+#pragma unroll
+      for (int q = 0; q < XB; ++q) {
+        float wv[CPL];
+        gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int e = 0; e < CPL; ++e) acc[r][e] = __builtin_fmaf(xc[r][q], wv[e], acc[r][e]);
+      }
+      if (s0 + XB < GV_CH) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+#pragma unroll
+          for (int q = 0; q < XB; ++q) xc[r][q] = xn[r][q];
+      }
+    }
+  }
+}
+
+// OP_NT (the LM layout W[n][k]): lane l owns output column j0 + l and walks its own W row,
+// contiguous in k, 16 bytes per load (VEC: 4 / 8 / 16 steps per load for f32 / bf16 / int8) or one
+// element per load.  A piece of up to 128 steps of the leaf is requested with one buffer
+// resource starting at row j0, step p0 (bounded by the operand's end: rows past n read zeros)
+// and immediate offsets, then consumed in order.  x is read XB steps at a time, one batch ahead.
+template <int BT, int MR, bool VEC, bool FULL>
+__device__ __forceinline__ void gv_steps_nt(float (&acc)[MR][1], const uint32_t (&buf)[VEC ? GV_CH * Elem<BT>::bytes / 4 : GV_CH],
+                                            const float* __restrict__ x, int64_t k, int64_t p0, int nrow, int m,
+                                            float sc) {
+  constexpr int EB = Elem<BT>::bytes;
+  constexpr int XB = MR <= 2 ? 16 : 32 / MR;
+  float xc[MR][XB], xn[MR][XB];
+  gv_load_x<MR, XB, FULL>(xc, x, k, p0, 0, m);
+#pragma unroll
+  for (int b = 0; b < GV_CH / XB; ++b) {
+    if (b + 1 < GV_CH / XB) gv_load_x<MR, XB, FULL>(xn, x, k, p0, (b + 1) * XB, m);
+#pragma unroll
+    for (int q = 0; q < XB; ++q) {
+      const int i = b * XB + q;
+      if (!FULL && i >= nrow) continue;  // uniform
+      float wv;
+      if constexpr (VEC) {
+        const uint32_t u = buf[i * EB / 4];
+        if constexpr (BT == T_F32) wv = __uint_as_float(u);
+        else if constexpr (BT == T_BF16) wv = __uint_as_float((i & 1) ? (u & 0xFFFF0000u) : (u << 16));
+        else wv = (float)((int32_t)(u << (24 - 8 * (i & 3))) >> 24) * sc;
+      } else {
+        const uint32_t u = buf[i];
+        if constexpr (BT == T_F32) wv = __uint_as_float(u);
+        else if constexpr (BT == T_BF16) wv = __uint_as_float(u << 16);
+        else wv = (float)(int32_t)(int8_t)(uint8_t)u * sc;
+      }
+#pragma unroll
+      for (int r = 0; r < MR; ++r) acc[r][0] = __builtin_fmaf(xc[r][q], wv, acc[r][0]);
+    }
+    if (b + 1 < GV_CH / XB) {
+#pragma unroll
+      for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int q = 0; q < XB; ++q) xc[r][q] = xn[r][q];
+    }
+  }
+}
+
+template <int BT, int MR, bool VEC>
+__device__ __forceinline__ void gv_leaf_nt(float (&acc)[MR][1], const char* w, int64_t n, int64_t k, int64_t j0,
+                                           int64_t kb, int64_t ke, const float* __restrict__ x, int m, float sc,
+                                           int lane) {
+  constexpr int EB = Elem<BT>::bytes;
+  constexpr int NW = VEC ? GV_CH * EB / 4 : GV_CH;  // words per piece
+  const int64_t total = n * k * EB;
+  const int voff = (int)(lane * k * EB);  // the host keeps 64 * k * bytes below 2^31
+  for (int64_t p0 = kb; p0 < ke; p0 += GV_CH) {
+    const int64_t off = (j0 * k + p0) * EB;
+    const int64_t rem = total - off;
+    const int nrec = rem <= 0 ? 0 : (rem > 0x7FFFFFFF ? 0x7FFFFFFF : (int)rem);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(w + (rem > 0 ? off : 0)), (short)0, nrec, RSRC_WORD3);
+    uint32_t buf[NW];
+    if constexpr (VEC) {
+#pragma unroll
+      for (int l = 0; l < NW / 4; ++l) {
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + l * 16, 0, 0);
+        buf[4 * l] = v[0]; buf[4 * l + 1] = v[1]; buf[4 * l + 2] = v[2]; buf[4 * l + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < GV_CH; ++i) {
+        if constexpr (BT == T_F32) buf[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + i * 4, 0, 0);
+        else if constexpr (BT == T_BF16) buf[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff + i * 2, 0, 0);
+        else buf[i] = __builtin_amdgcn_raw_buffer_load_b8(rs, voff + i, 0, 0);
+      }
+    }
+    const int64_t nrow = ke - p0;
+    if (nrow >= GV_CH) gv_steps_nt<BT, MR, VEC, true>(acc, buf, x, k, p0, GV_CH, m, sc);
+    else gv_steps_nt<BT, MR, VEC, false>(acc, buf, x, k, p0, (int)nrow, m, sc);
+  }
+}
+
+// One skinny product: OP_NN (W[k][n], FULLLEAF: every leaf exactly 128 rows) or OP_NT (W[n][k]).
+template <int BT, int MR, bool VEC, bool FULLLEAF, bool NT>
+__device__ __forceinline__ void gemv_body(const GemvArgs& g, const float* __restrict__ x) {
+  constexpr int CPL = GvCols<BT, NT>::cpl;
+  constexpr int COLS = GvCols<BT, NT>::cols;
+  constexpr int EB = Elem<BT>::bytes;
+  __shared__ float part[GV_LEAVES][MR][COLS];
+  __shared__ unsigned int last_flag;
+
+  set_flush_inputs_mode();
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: leaf and k range too
+  const int64_t cg = blockIdx.x % g.ncg;
+  const int64_t grp = blockIdx.x / g.ncg;
+  const int64_t t = grp * GV_LEAVES + wave;  // this wave's leaf
+  const int m = (int)g.m;
+
+  float acc[MR][CPL];
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) acc[r][e] = 0.f;
+
+  if constexpr (NT) {
+    if (t < g.nleaves) {
+      const int64_t j0 = cg * COLS;
+      float sc = 1.f;
+      if constexpr (BT == T_I8) sc = g.scales[j0 + lane < g.n ? j0 + lane : g.n - 1];
+      const int64_t kb = t * g.leaf;
+      const int64_t ke = kb + g.leaf < g.k ? kb + g.leaf : g.k;
+      gv_leaf_nt<BT, MR, VEC>(acc, static_cast<const char*>(g.w), g.n, g.k, j0, kb, ke, x, m, sc, lane);
+    }
+  } else if (t < g.nleaves) {
+    // this lane's columns, clamped into the operand (their cells are never stored)
+    int64_t c0 = cg * COLS + lane * CPL;
+    uint32_t coff[CPL];
+    float sc[CPL];
+    if constexpr (VEC) {
+      if (c0 >= g.n) c0 = g.n - CPL;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) coff[e] = (uint32_t)((c0 + e) * EB);
+    } else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) coff[e] = (uint32_t)((c0 + e < g.n ? c0 + e : g.n - 1) * EB);
+    }
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      sc[e] = 1.f;
+      if constexpr (BT == T_I8) sc[e] = g.scales[coff[e]];  // EB == 1: the offset is the column
+    }
+    const char* w = static_cast<const char*>(g.w);
+    const uint32_t loff = coff[0];
+    const int64_t rowbytes = g.n * EB;
+    const int64_t kb = t * g.leaf;
+    const int64_t ke = kb + g.leaf < g.k ? kb + g.leaf : g.k;
+    const int64_t klast = ke - 1;
+
+    if constexpr (FULLLEAF) {
+      gv_leaf_full<BT, MR>(acc, w + kb * rowbytes, loff, (int)rowbytes, x + kb, g.k, m, sc);
+    } else {
+      // The general case: the leaf's rows in pieces of GV_CH (one piece unless the leaf is
+      // longer than 128); every row of a piece is requested before its first step, and the
+      // steps consume them in order as they land.
+      uint32_t buf[GV_CH];
+      for (int64_t p0 = kb; p0 < ke; p0 += GV_CH) {
+        const int64_t nrow = ke - p0;
+        gv_load<BT, VEC>(buf, w, loff, coff, rowbytes, p0, klast);
+        if (nrow >= GV_CH) gv_steps<BT, MR, true>(acc, buf, x, g.k, p0, GV_CH, m, sc);
+        else gv_steps<BT, MR, false>(acc, buf, x, g.k, p0, (int)nrow, m, sc);
+      }
+    }
+  }
+
+  // The group's root: the tree over its (up to GV_LEAVES) leaf partials, through LDS.
+#pragma unroll
+  for (int r = 0; r < MR; ++r)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) part[wave][r][lane * CPL + e] = acc[r][e];
+  __syncthreads();
+  const int64_t left = g.nleaves - grp * GV_LEAVES;
+  const int cnt = left < GV_LEAVES ? (int)left : GV_LEAVES;
+  for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
+    const int r = cell / COLS, col = cell % COLS;
+    const int64_t j = cg * COLS + col;
+    if (r >= m || j >= g.n) continue;
+    float y = part[0][r][col];
+    if (cnt >= 2) y = y + part[1][r][col];           // leaves 0,1 paired
+    if (cnt == 3) y = y + part[2][r][col];           // leaf 2 carried, then joined
+    if (cnt == 4) y = y + (part[2][r][col] + part[3][r][col]);
+    if (g.ngroups == 1) {
+      if (g.bias) y = y + g.bias[j];  // ftz(C) + ftz(b) by the input flush
+      g.c[r * g.n + j] = store_word(y);
+    } else {
+      __hip_atomic_store(&g.ws[(grp * g.m + r) * g.n + j], y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (g.ngroups == 1) return;
+
+  // Count this group's roots in; the workgroup that completes the count folds.  The roots
+  // are device-coherent stores, complete (vmcnt) before the count is published.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int prev = __hip_atomic_fetch_add(&g.counter[cg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = prev + 1 == (unsigned int)g.ngroups ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  const int64_t stride = g.m * g.n;
+  constexpr int CPT = (MR * COLS + GV_THREADS - 1) / GV_THREADS;  // cells per thread
+  if (g.ngroups <= GV_FEW_GROUPS) {
+    // every root of every cell of this thread requested at once, then folded
+    float v[CPT][GV_FEW_GROUPS];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int cell = tid + c * GV_THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (cell >= MR * COLS || r >= m || j >= g.n) continue;
+#pragma unroll
+      for (int e = 0; e < GV_FEW_GROUPS; ++e)
+        if (e < g.ngroups)
+          v[c][e] = __hip_atomic_load(g.ws + (e * g.m + r) * g.n + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int cell = tid + c * GV_THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (cell >= MR * COLS || r >= m || j >= g.n) continue;
+      StackF stk;
+      const int P = (int)g.ngroups;
+#pragma unroll
+      for (int e = 0; e + 1 < GV_FEW_GROUPS; ++e)
+        if (e + 1 < P) stk.push(v[c][e], e);
+      float y = v[c][0];
+#pragma unroll
+      for (int e = 1; e < GV_FEW_GROUPS; ++e)
+        if (e == P - 1) y = v[c][e];
+      y = stk.root(y, P - 1);
+      if (g.bias) y = y + g.bias[j];
+      g.c[r * g.n + j] = store_word(y);
+    }
+  } else {
+    for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (r >= m || j >= g.n) continue;
+      float y = fold_roots(g.ws + r * g.n + j, g.ngroups, stride);
+      if (g.bias) y = y + g.bias[j];
+      g.c[r * g.n + j] = store_word(y);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&g.counter[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace mlg

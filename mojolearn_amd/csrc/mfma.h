@@ -1,0 +1,52 @@
+// The MFMA GEMM kernel (gemm_mfma.hip): tile constants, argument block, launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlg {
+
+// Tiling: 512 threads = 8 waves (2 per SIMD); workgroup tile 128 x 128 cells; each wave owns
+// 64 rows x 32 columns = one v_mfma_f32_32x32x1_2b_f32 per k step (block 0 = rows 0-31,
+// block 1 = rows 32-63, both against the same 32 columns).  K is staged through LDS in
+// KT = 32-step slices, three buffers (loads issued two slices ahead).  Operands travel
+// HBM -> LDS with buffer loads straight into LDS (16 bytes per lane, no registers) in their
+// stored element type; bf16 widening and int8 x column-scale dequantisation happen when a
+// lane reads its MFMA operand out of LDS.
+constexpr int NTHREADS = 512;
+constexpr int NWAVES = NTHREADS / 64;
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int KT = 32;
+constexpr int SLICE_BYTES = BM * KT * 4;  // one operand slice at float32: 16 KB
+constexpr int NBUF = 3;                   // slices in LDS: loads run two slices ahead
+constexpr int MAX_GROUP_LEAVES = 32;      // one group's leaves fold in registers + one LDS slot
+
+struct GemmArgs {
+  float* c;
+  const void* a;      // stored operands: 16-byte aligned, rows a multiple of 16 bytes
+  const void* b;
+  const float* scales;
+  const float* bias;
+  float* ws;          // group roots [ngroups][m][n] when ngroups > 1
+  int64_t m, n, k;
+  int64_t leaf;       // L
+  int64_t nleaves;    // P
+  int64_t group;      // leaves per group (power of two, <= 32)
+  int64_t ngroups;
+  int64_t a_pitch, b_pitch;  // stored row lengths in elements
+  int64_t a_bytes, b_bytes;  // stored operand sizes
+  int tiles_n;
+};
+
+// Launch gemm_mfma_kernel<op, a_type, b_type> on `grid` (tiles, leaf groups).
+hipError_t launch_mfma(const GemmArgs& g, int op, int a_type, int b_type, dim3 grid, hipStream_t stream);
+
+// Copy [rows][cols] elements of `eb` bytes into [rows][pitch], zero padding.
+hipError_t launch_repack(char* dst, const char* src, int64_t rows, int64_t cols, int64_t pitch, int eb,
+                         hipStream_t stream);
+
+// Fold `ngroups` group roots ws[g][m][n] per cell (0 groups: store +0.0), add bias, store.
+hipError_t launch_fold_groups(float* c, const float* ws, const float* bias, int64_t m, int64_t n, int64_t ngroups,
+                              hipStream_t stream);
+
+}  // namespace mlg

@@ -239,6 +239,38 @@ def test_skinny_m(oracle, shape, wt):
         assert_bits(got2.cpu().numpy(), oracle.nan_canon(want), "second call")
 
 
+GEMV_NT_SHAPES = GEMV_SHAPES + [(1, 64, 128), (4, 65, 256), (1, 130, 200)]
+
+
+@pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
+@pytest.mark.parametrize("shape", GEMV_NT_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_NT_SHAPES])
+def test_skinny_m_nt(oracle, shape, wt):
+    """The skinny-M path in the LM layout (OP_NT, W[n][k]): a lane per output column walking
+    its own W row, 16-byte loads when rows and leaf starts are 16-byte aligned, element loads
+    otherwise; the same leaf groups and fold as OP_NN."""
+    D = _dev()
+    m, n, k = shape
+    rng = np.random.default_rng(m + n + k + 1)
+    x = _values(rng, (m, k), "wide")
+    print(f"skinny NT {wt} m={m} n={n} k={k}", flush=True)
+    tx = torch.from_numpy(x).to(DEV)
+    if wt == "f32":
+        w = _values(rng, (n, k), "wide")
+        got = D.gemm(tx, torch.from_numpy(w).to(DEV), op=D.OP_NT)
+        want = oracle.gemm_fast(x, w, oracle.OP_NT)
+    elif wt == "bf16":
+        wb = oracle.bf16_narrow(_values(rng, (n, k), "wide"))
+        got = D.gemm_bf16w(tx, torch.from_numpy(wb.view(np.int16)).to(DEV), op=D.OP_NT)
+        want = oracle.gemm_fast(x, oracle.bf16_widen(wb), oracle.OP_NT)
+    else:
+        codes = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        got = D.gemm_int8w(tx, torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV), op=D.OP_NT)
+        want = oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, oracle.OP_NT), oracle.OP_NT)
+    torch.cuda.synchronize()
+    assert_bits(got.cpu().numpy(), oracle.nan_canon(want), f"skinny NT {wt} {shape}")
+
+
 @pytest.mark.parametrize("case", ["skinny_i8", "mfma_groups", "mfma_bias"])
 def test_plan_in_graph_replays(oracle, case):
     """A Plan (caller workspace, no allocation per call) captured in a HIP graph: every replay,
