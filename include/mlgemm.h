@@ -43,7 +43,13 @@ typedef void (*mlg_sink_t)(int64_t ctx, int64_t utf8_ptr, int64_t len);
  *                                                                       Y = ftz(ftz(C) + ftz(bias[j]))
  *                                                                       (transformer/impl/llama/
  *                                                                       modeling_llama.mojo:3979-3989)
- * Ops 2-7 and 10 (int8i32 / int15i64 profiles, from_f16) are refused by name.
+ *   2   [c, qa, ea, qb, eb]         [m, n, k]                  m*n      gemm_int8, profile int8i32.v1,
+ *                                                                       OP_NT: codes int8 row-major, one
+ *                                                                       int32 exponent per row; k <= 131072
+ *                                                                       (gemm/linalg_native.mojo:258-321)
+ *   3   [codes_i8, exps_i32, x]     [rows, cols]               rows*cols quantize_int8 (L-3, L-4; :323-357)
+ *   4   [y_f32, codes_i8, exps_i32] [rows, cols]               rows*cols dequantize_int8 (L-6; :359-393)
+ * Ops 5-7 and 10 (int15i64 profile, from_f16) are refused by name.
  */
 int64_t linalg_native_v1(int64_t op, int64_t addrs, int64_t n_addrs, int64_t ints, int64_t n_ints,
                          int64_t floats, int64_t n_floats, int64_t result, int64_t err_ctx,
@@ -98,6 +104,22 @@ int64_t mlg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t op, in
 /* L-1 / L-2 conversions on device buffers (checks/numerics.mojo:1548-1574). */
 int mlg_bf16_widen(float* out, const uint16_t* in, int64_t count, void* stream);
 int mlg_bf16_narrow(uint16_t* out, const float* in, int64_t count, void* stream);
+
+/* Profile mojolearn.identical.gemm.int8i32.v1 on device buffers (gemm/IDENTICAL_LOWBIT_CONTRACT.md
+ * L-3..L-7; the reference's device entries identical_gemm_int8_into, quantize_rows_int8_device and
+ * dequantize_rows_int8_device, gemm/linalg_native.mojo:258-393).
+ * quantize: per row e = floor(log2 absmax) - 6 (0 for an all-zero row) and codes
+ *   clamp(rne(ftz(x) * 2^-e), -127, 127), a NaN coding to 0.
+ * dequantize: out = ftz(code * 2^e) per row.
+ * gemm: OP_NT, C[i][j] = ftz(f32(sum_p qa[i][p] qb[j][p]) * 2^(ea[i] + eb[j])) with the sum exact in
+ *   Int32 and converted by the pinned split (L-5); 1 <= k <= 131072.  Allocates a repack buffer from
+ *   the stream-ordered pool only when k is not a multiple of 16 or a base is not 16-byte aligned. */
+int mlg_int8_quantize(int8_t* codes, int32_t* exponents, const float* x, int64_t rows, int64_t cols,
+                      void* stream);
+int mlg_int8_dequantize(float* out, const int8_t* codes, const int32_t* exponents, int64_t rows,
+                        int64_t cols, void* stream);
+int mlg_gemm_int8i32(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
+                     int64_t m, int64_t n, int64_t k, void* stream);
 
 /* The message of the calling thread's last failed mlg_* call ("" if none). */
 const char* mlg_last_error(void);

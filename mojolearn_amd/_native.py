@@ -47,6 +47,12 @@ def lib():
         L.mlg_bf16_widen.restype = ctypes.c_int
         L.mlg_bf16_narrow.argtypes = [vp, vp, i64, vp]
         L.mlg_bf16_narrow.restype = ctypes.c_int
+        L.mlg_int8_quantize.argtypes = [vp, vp, vp, i64, i64, vp]
+        L.mlg_int8_quantize.restype = ctypes.c_int
+        L.mlg_int8_dequantize.argtypes = [vp, vp, vp, i64, i64, vp]
+        L.mlg_int8_dequantize.restype = ctypes.c_int
+        L.mlg_gemm_int8i32.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, vp]
+        L.mlg_gemm_int8i32.restype = ctypes.c_int
         L.mlg_last_error.argtypes = []
         L.mlg_last_error.restype = ctypes.c_char_p
         for name in ("mlg_numeric_mode", "mlg_profile_version", "mlg_lowbit_profile_version"):

@@ -18,6 +18,7 @@
 #include "../../include/mlgemm.h"
 #include "contract.h"
 #include "kernels.h"
+#include "q8.h"
 
 namespace {
 
@@ -154,7 +155,7 @@ struct DeviceBuf {
 };
 
 struct HostPool {
-  DeviceBuf c, a, b, x;
+  DeviceBuf c, a, b, x, y, w;
   hipStream_t stream = nullptr;
 };
 
@@ -182,7 +183,8 @@ struct Lease {
     if (pooled) {
       g_pool_busy.store(0);
     } else {
-      fresh.c.release(); fresh.a.release(); fresh.b.release(); fresh.x.release();
+      fresh.c.release(); fresh.a.release(); fresh.b.release(); fresh.x.release(); fresh.y.release();
+      fresh.w.release();
       if (fresh.stream) (void)hipStreamDestroy(fresh.stream);
     }
   }
@@ -255,6 +257,62 @@ int64_t host_convert(const std::vector<int64_t>& ad, const std::vector<int64_t>&
   return count;
 }
 
+// ---- profile int8i32.v1 on host pointers (gemm/linalg_native.mojo:258-393; refusals :114-121)
+int64_t host_q8_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr) {
+  if (pr.size() != 3) throw Fail("gemm_int8: params must contain 3 values (m, n, k), got " + std::to_string(pr.size()));
+  const int64_t m = pr[0], n = pr[1], k = pr[2];
+  if (m <= 0 || n <= 0 || k <= 0)
+    throw Fail("gemm_int8: m, n and k must all be positive, got m=" + std::to_string(m) + " n=" +
+               std::to_string(n) + " k=" + std::to_string(k));
+  if (k > mlg::INT8_MAX_K)
+    throw Fail("gemm_int8: k must be at most " + std::to_string(mlg::INT8_MAX_K) + " (contract L-7), got " +
+               std::to_string(k));
+  Lease lease;
+  HostPool& P = *lease.pool;
+  float* dc = (float*)P.c.get((size_t)(m * n) * 4);
+  int8_t* dqa = (int8_t*)P.a.get((size_t)(m * k));
+  int8_t* dqb = (int8_t*)P.b.get((size_t)(n * k));
+  int32_t* dea = (int32_t*)P.x.get((size_t)m * 4);
+  int32_t* deb = (int32_t*)P.y.get((size_t)n * 4);
+  up(dqa, (const void*)ad[1], (size_t)(m * k), P.stream);
+  up(dea, (const void*)ad[2], (size_t)m * 4, P.stream);
+  up(dqb, (const void*)ad[3], (size_t)(n * k), P.stream);
+  up(deb, (const void*)ad[4], (size_t)n * 4, P.stream);
+  const int64_t wsb = mlg::q8_workspace_bytes(dqa, dqb, m, n, k);
+  void* dws = wsb > 0 ? P.w.get((size_t)wsb) : nullptr;
+  hip_check(mlg::run_q8_gemm(dc, dqa, dea, dqb, deb, m, n, k, dws, num_cus_of_current_device(), P.stream),
+            "gemm_int8 launch");
+  down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  return m * n;
+}
+
+int64_t host_q8_convert(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr, bool quantize) {
+  const char* who = quantize ? "quantize_int8" : "dequantize_int8";
+  if (pr.size() != 2) throw Fail(std::string(who) + ": params must contain 2 values (rows, cols), got " + std::to_string(pr.size()));
+  const int64_t rows = pr[0], cols = pr[1];
+  if (rows <= 0 || cols <= 0)
+    throw Fail(std::string(who) + ": rows and cols must be positive, got " + std::to_string(rows) + " x " + std::to_string(cols));
+  Lease lease;
+  HostPool& P = *lease.pool;
+  float* df = (float*)P.c.get((size_t)(rows * cols) * 4);
+  int8_t* dq = (int8_t*)P.a.get((size_t)(rows * cols));
+  int32_t* de = (int32_t*)P.x.get((size_t)rows * 4);
+  if (quantize) {  // addrs [codes, exponents, x]
+    up(df, (const void*)ad[2], (size_t)(rows * cols) * 4, P.stream);
+    hip_check(mlg::run_q8_quantize(dq, de, df, rows, cols, P.stream), "quantize_int8 launch");
+    down((void*)ad[0], dq, (size_t)(rows * cols), P.stream);
+    down((void*)ad[1], de, (size_t)rows * 4, P.stream);
+  } else {  // addrs [y, codes, exponents]
+    up(dq, (const void*)ad[1], (size_t)(rows * cols), P.stream);
+    up(de, (const void*)ad[2], (size_t)rows * 4, P.stream);
+    hip_check(mlg::run_q8_dequantize(df, dq, de, rows, cols, P.stream), "dequantize_int8 launch");
+    down((void*)ad[0], df, (size_t)(rows * cols) * 4, P.stream);
+  }
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  return rows * cols;
+}
+
 std::vector<int64_t> words(int64_t addr, int64_t n) {
   if (n < 0 || (n > 0 && addr == 0)) throw Fail("linalg native ABI: invalid descriptor span");
   std::vector<int64_t> v((size_t)n);
@@ -296,9 +354,18 @@ int64_t native_operation(int64_t op, const std::vector<int64_t>& a, const std::v
       if (a.size() != 4) throw Fail("linalg native ABI: invalid gemm_bias address count");
       if (p.size() != 4) throw Fail("gemm_bias: params must contain 4 values (m, n, k, op), got " + std::to_string(p.size()));
       return host_gemm(a, p, mlg::T_F32, mlg::T_F32, true);
-    case 2: case 3: case 4: case 5: case 6: case 7: case 10:
+    case 2:
+      if (a.size() != 5) throw Fail("linalg native ABI: invalid gemm_int8 address count");
+      return host_q8_gemm(a, p);
+    case 3:
+      if (a.size() != 3) throw Fail("linalg native ABI: invalid quantize_int8 address count");
+      return host_q8_convert(a, p, true);
+    case 4:
+      if (a.size() != 3) throw Fail("linalg native ABI: invalid dequantize_int8 address count");
+      return host_q8_convert(a, p, false);
+    case 5: case 6: case 7: case 10:
       throw Fail("linalg native ABI: operation " + std::to_string(op) +
-                 " (int8i32 / int15i64 profiles, from_f16) is not part of this build's identical fp32 GEMM path");
+                 " (int15i64 profile, from_f16) is not part of this build");
     default:
       throw Fail("linalg native ABI: unknown operation");
   }
@@ -391,6 +458,46 @@ int mlg_bf16_widen(float* out, const uint16_t* in, int64_t count, void* stream) 
 
 int mlg_bf16_narrow(uint16_t* out, const float* in, int64_t count, void* stream) {
   return guarded([&] { hip_check(mlg::run_bf16_narrow(out, in, count, (hipStream_t)stream), "to_bf16 launch"); });
+}
+
+int mlg_int8_quantize(int8_t* codes, int32_t* exponents, const float* x, int64_t rows, int64_t cols, void* stream) {
+  return guarded([&] {
+    if (rows < 0 || cols < 0) throw Fail("quantize_int8: rows and cols must be >= 0");
+    if (rows > 0 && cols > 0 && (!codes || !exponents || !x)) throw Fail("quantize_int8: null pointer");
+    hip_check(mlg::run_q8_quantize(codes, exponents, x, rows, cols, (hipStream_t)stream), "quantize_int8 launch");
+  });
+}
+
+int mlg_int8_dequantize(float* out, const int8_t* codes, const int32_t* exponents, int64_t rows, int64_t cols,
+                        void* stream) {
+  return guarded([&] {
+    if (rows < 0 || cols < 0) throw Fail("dequantize_int8: rows and cols must be >= 0");
+    if (rows > 0 && cols > 0 && (!codes || !exponents || !out)) throw Fail("dequantize_int8: null pointer");
+    hip_check(mlg::run_q8_dequantize(out, codes, exponents, rows, cols, (hipStream_t)stream), "dequantize_int8 launch");
+  });
+}
+
+int mlg_gemm_int8i32(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
+                     int64_t m, int64_t n, int64_t k, void* stream) {
+  return guarded([&] {
+    if (m <= 0 || n <= 0 || k <= 0)
+      throw Fail("gemm_int8: m, n and k must all be positive, got m=" + std::to_string(m) + " n=" +
+                 std::to_string(n) + " k=" + std::to_string(k));
+    if (k > mlg::INT8_MAX_K)
+      throw Fail("gemm_int8: k must be at most " + std::to_string(mlg::INT8_MAX_K) + " (contract L-7), got " +
+                 std::to_string(k));
+    if (!c || !ea || !eb || !qa || !qb) throw Fail("gemm_int8: null operand pointer");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t wsb = mlg::q8_workspace_bytes(qa, qb, m, n, k);
+    void* ws = nullptr;
+    if (wsb > 0) hip_check(hipMallocAsync(&ws, (size_t)wsb, s), "hipMallocAsync");
+    hipError_t e = mlg::run_q8_gemm(c, qa, ea, qb, eb, m, n, k, ws, num_cus_of_current_device(), s);
+    if (ws) {
+      hipError_t f = hipFreeAsync(ws, s);
+      if (e == hipSuccess) e = f;
+    }
+    hip_check(e, "gemm_int8 launch");
+  });
 }
 
 const char* mlg_last_error(void) { return g_last_error.c_str(); }

@@ -1,0 +1,288 @@
+// gfx950 kernels of the profile mojolearn.identical.gemm.int8i32.v1
+// (gemm/IDENTICAL_LOWBIT_CONTRACT.md L-3..L-7): the row quantizer, the dequantizer and the OP_NT
+// product on the integer matrix unit.
+//
+// The product's only arithmetic before the store is an integer sum of int8 x int8 products in an
+// Int32 that cannot overflow (k <= 131072), so the order in which the matrix unit adds them is
+// scheduling (L-9's construction): v_mfma_i32_32x32x32_i8 gives the same Int32 as the oracle's
+// ascending loop.  Codes past k are masked to zero (a zero code adds nothing).  The float steps,
+// L-5's split conversion and L-6's power-of-two multiply and flush, run once per cell at the store.
+#include "device_common.h"
+#include "lds_stage.h"
+#include "mfma.h"
+#include "q8.h"
+
+namespace mlg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// checks/numerics.mojo:1589-1598 pow2_f32: 2^e from its exponent field; above 127 the infinity,
+// below -126 +0.0.
+__device__ __forceinline__ float q8_pow2(int64_t e) {
+  if (e > 127) return __uint_as_float(0x7F800000u);
+  if (e < -126) return 0.f;
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// checks/numerics.mojo:262-268: a subnormal becomes the zero of its own sign.
+__device__ __forceinline__ float q8_ftz(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x7F800000u) == 0u ? __uint_as_float(u & 0x80000000u) : x;
+}
+
+// checks/numerics.mojo:1609-1630 i32_to_f32_pinned (L-5): two exact conversions (a 20-bit high
+// part, a 12-bit low part), an exact scaling by 2^12, one IEEE addition.
+__device__ __forceinline__ float q8_i32_to_f32(int32_t v) {
+  const bool neg = v < 0;
+  const uint32_t mag = neg ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
+  const float hi = (float)(mag >> 12);
+  const float lo = (float)(mag & 0xFFFu);
+  const float r = hi * 4096.0f + lo;
+  return neg ? -r : r;
+}
+
+// checks/numerics.mojo:1671-1677 dequant_int8_pinned (L-6), then the store's NaN canonicalisation.
+__device__ __forceinline__ float q8_dequant(int32_t acc, int64_t e_sum) {
+  return store_word(q8_ftz(q8_i32_to_f32(acc) * q8_pow2(e_sum)));
+}
+
+// ---------------------------------------------------------------------------
+// Quantizer (L-3, L-4; checks/numerics.mojo:1638-1668, gemm/host/gemm_lowbit_oracle.mojo:171-198):
+// one 256-thread workgroup per row.  The absmax is a maximum (exact, order-free), so a tree
+// reduction gives the oracle's value; a NaN never wins a comparison.
+constexpr int Q8_THREADS = 256;
+
+__device__ __forceinline__ float q8_absmax_step(float best, float x) {
+  float v = q8_ftz(x);
+  if (v < 0.f) v = -v;
+  return v > best ? v : best;
+}
+
+__device__ __forceinline__ int8_t q8_code(float x, int e) {
+  if (x != x) return 0;
+  const float s = q8_ftz(q8_ftz(x) * q8_pow2(-(int64_t)e));
+  const float magic = 12582912.0f;  // checks/numerics.mojo:1577-1586 f32_round_half_even
+  float r = s >= 0.f ? (s + magic) - magic : (s - magic) + magic;
+  if (r != r) return 0;  // 0 * 2^-e with 2^-e infinite (absmax below 2^-121): the reference's Int(NaN) -> 0
+  if (r > 127.f) r = 127.f;
+  if (r < -127.f) r = -127.f;
+  return (int8_t)(int)r;
+}
+
+__global__ void __launch_bounds__(Q8_THREADS) q8_quantize_kernel(int8_t* codes, int32_t* exps, const float* x,
+                                                                 int64_t cols) {
+  __shared__ float wbest[Q8_THREADS / 64];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * cols;
+  float best = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += Q8_THREADS) best = q8_absmax_step(best, xr[c]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(best, off, 64);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+  __syncthreads();
+  best = wbest[0];
+#pragma unroll
+  for (int w = 1; w < Q8_THREADS / 64; ++w) best = wbest[w] > best ? wbest[w] : best;
+  // int8_row_exponent: floor(log2 absmax) - 6 from the exponent field; 0 for a zero row
+  const float a = q8_ftz(best);
+  const int e = (a == 0.f || a != a) ? 0 : (int)((__float_as_uint(a) >> 23) & 0xFFu) - 127 - 6;
+  if (threadIdx.x == 0) exps[row] = e;
+  int8_t* cr = codes + row * cols;
+  for (int64_t c = threadIdx.x; c < cols; c += Q8_THREADS) cr[c] = q8_code(xr[c], e);
+}
+
+__global__ void q8_dequantize_kernel(float* out, const int8_t* codes, const int32_t* exps, int64_t rows,
+                                     int64_t cols) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * cols) return;
+  out[i] = q8_dequant((int32_t)codes[i], exps[i / cols]);
+}
+
+// ---------------------------------------------------------------------------
+// The product.  Tiling as the fp32 MFMA kernel: 512 threads, a 128 x 128 cell tile, wave (wr, wc)
+// owns rows wr*64 .. +63 (two 32-row blocks) and columns wc*32 .. +31.  Both operands store k
+// contiguously (OP_NT), so a slice of 128 codes per row is staged exactly like an index-major
+// float32 slice of 32 words (16-byte chunks, swizzled rows) and read 16 codes per lane: lane l of
+// v_mfma_i32_32x32x32_i8 gives row / column l % 32 and codes 16 (l / 32) .. +15 of the 32-code
+// step, the same k range for both operands.
+struct Q8Args {
+  float* c;
+  const void* qa;      // [m][pitch] codes (pitch a multiple of 16 bytes)
+  const void* qb;      // [n][pitch]
+  const int32_t* ea;
+  const int32_t* eb;
+  int64_t m, n, k;
+  int64_t pitch_words;  // pitch / 4
+  int64_t a_bytes, b_bytes;
+  int tiles_n;
+};
+
+constexpr int Q8_KS = KT * 4;  // codes per slice: 128
+
+template <bool MASK>
+__device__ __forceinline__ void q8_slice(v16i (&acc)[2], const char* la, const char* lb, int wr, int lane,
+                                         int bcol, int64_t valid) {
+#pragma unroll
+  for (int q = 0; q < Q8_KS / 32; ++q) {
+    const int s = 8 * q + 4 * (lane >> 5);  // word offset of this lane's 16 codes in the row
+    const v4i b4 = __builtin_bit_cast(v4i, read4<T_F32, true>(lb, bcol, s, 1.f));
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      v4i a4 = __builtin_bit_cast(v4i, read4<T_F32, true>(la, wr * 64 + 32 * blk + (lane & 31), s, 1.f));
+      if constexpr (MASK) {
+        // codes at or past k are zero (they may hold the next row's bytes); 0 < valid < 128 here
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int d = (int)valid - 4 * (s + w);  // codes of this word below k
+          const uint32_t keep = d >= 4 ? 0xFFFFFFFFu : (d <= 0 ? 0u : 0xFFFFFFFFu >> (8 * (4 - d)));
+          a4[w] = (int)((uint32_t)a4[w] & keep);
+        }
+      }
+      acc[blk] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, acc[blk], 0, 0, 0);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(NTHREADS) q8_gemm_kernel(Q8Args g) {
+  __shared__ __attribute__((aligned(1024))) char lds0[2][SLICE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds1[2][SLICE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds2[2][SLICE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 2;
+  const int wc = wave & 3;
+  const int64_t i0 = (int64_t)(blockIdx.x / g.tiles_n) * BM;
+  const int64_t j0 = (int64_t)(blockIdx.x % g.tiles_n) * BN;
+  const int64_t nslices = (g.k + Q8_KS - 1) / Q8_KS;
+
+  DirectLoader<T_F32, true> lda, ldb;
+  lda.init(g.pitch_words, wave, lane);
+  ldb.init(g.pitch_words, wave, lane);
+  constexpr int LPS = 2 * Slice<T_F32, true>::PER_WAVE;
+  constexpr int WAIT_ONE_BEHIND = (LPS & 0xF) | ((LPS >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+  lda.issue(lds0[0], g.qa, g.a_bytes, g.pitch_words, i0, 0, wave);
+  ldb.issue(lds0[1], g.qb, g.b_bytes, g.pitch_words, j0, 0, wave);
+  lda.issue(lds1[0], g.qa, g.a_bytes, g.pitch_words, i0, KT, wave);
+  ldb.issue(lds1[1], g.qb, g.b_bytes, g.pitch_words, j0, KT, wave);
+
+  const int bcol = wc * 32 + (lane & 31);
+  v16i acc[2];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[blk][e] = 0;
+
+  __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND);
+  lds_barrier();
+
+  // Slice kt out of buffer CUR while slice kt + 2 loads into FILL (unrolled by three so the
+  // compiler sees distinct buffers); the last slice masks the codes past k.
+#define MLG_Q8_STEP(CUR, FILL)                                                                   \
+  do {                                                                                           \
+    lda.issue(FILL[0], g.qa, g.a_bytes, g.pitch_words, i0, (kt + 2) * KT, wave);                 \
+    ldb.issue(FILL[1], g.qb, g.b_bytes, g.pitch_words, j0, (kt + 2) * KT, wave);                 \
+    const int64_t valid = g.k - kt * Q8_KS;                                                      \
+    if (valid >= Q8_KS) q8_slice<false>(acc, CUR[0], CUR[1], wr, lane, bcol, valid);             \
+    else q8_slice<true>(acc, CUR[0], CUR[1], wr, lane, bcol, valid);                             \
+    __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND);                                                 \
+    lds_barrier();                                                                               \
+  } while (0)
+  for (int64_t kt = 0; kt < nslices;) {
+    MLG_Q8_STEP(lds0, lds2);
+    if (++kt >= nslices) break;
+    MLG_Q8_STEP(lds1, lds0);
+    if (++kt >= nslices) break;
+    MLG_Q8_STEP(lds2, lds1);
+    ++kt;
+  }
+#undef MLG_Q8_STEP
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load into LDS outlives the workgroup
+
+  const int64_t col = j0 + bcol;
+  if (col >= g.n) return;
+  const int64_t eb = g.eb[col];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = i0 + wr * 64 + 32 * blk + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+      if (row < g.m) g.c[row * g.n + col] = q8_dequant(acc[blk][r], (int64_t)g.ea[row] + eb);
+    }
+  }
+}
+
+__global__ void q8_repack_kernel(int8_t* dst, const int8_t* src, int64_t rows, int64_t k, int64_t pitch) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * pitch) return;
+  const int64_t r = i / pitch, c = i % pitch;
+  dst[i] = c < k ? src[r * k + c] : (int8_t)0;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+static bool q8_in_place(const void* p, int64_t k) { return k % 16 == 0 && ((uintptr_t)p % 16u) == 0; }
+static int64_t q8_pitch(int64_t k) { return (k + 15) / 16 * 16; }
+
+int64_t q8_workspace_bytes(const void* qa, const void* qb, int64_t m, int64_t n, int64_t k) {
+  int64_t bytes = 0;
+  if (!q8_in_place(qa, k)) bytes += (m * q8_pitch(k) + 255) / 256 * 256;
+  if (!q8_in_place(qb, k)) bytes += (n * q8_pitch(k) + 255) / 256 * 256;
+  return bytes;
+}
+
+hipError_t run_q8_quantize(int8_t* codes, int32_t* exps, const float* x, int64_t rows, int64_t cols,
+                           hipStream_t stream) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  hipLaunchKernelGGL(q8_quantize_kernel, dim3((unsigned)rows), dim3(Q8_THREADS), 0, stream, codes, exps, x, cols);
+  return hipGetLastError();
+}
+
+hipError_t run_q8_dequantize(float* out, const int8_t* codes, const int32_t* exps, int64_t rows, int64_t cols,
+                             hipStream_t stream) {
+  const int64_t total = rows * cols;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(q8_dequantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, out, codes,
+                     exps, rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
+                       int64_t m, int64_t n, int64_t k, void* ws, int num_cus, hipStream_t stream) {
+  (void)num_cus;
+  if (m <= 0 || n <= 0 || k <= 0 || k > INT8_MAX_K) return hipErrorInvalidValue;
+  const int64_t pitch = q8_pitch(k);
+  if (32 * pitch + Q8_KS >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  char* wsp = static_cast<char*>(ws);
+  const void* ops[2] = {qa, qb};
+  const int64_t rows[2] = {m, n};
+  for (int w = 0; w < 2; ++w) {
+    if (q8_in_place(ops[w], k)) continue;
+    if (wsp == nullptr) return hipErrorInvalidValue;
+    const int64_t total = rows[w] * pitch;
+    hipLaunchKernelGGL(q8_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<int8_t*>(wsp), static_cast<const int8_t*>(ops[w]), rows[w], k, pitch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    ops[w] = wsp;
+    wsp += (total + 255) / 256 * 256;
+  }
+  Q8Args g;
+  g.c = c; g.qa = ops[0]; g.qb = ops[1]; g.ea = ea; g.eb = eb;
+  g.m = m; g.n = n; g.k = k;
+  g.pitch_words = pitch / 4;
+  g.a_bytes = m * pitch;
+  g.b_bytes = n * pitch;
+  const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  g.tiles_n = (int)tn;
+  hipLaunchKernelGGL(q8_gemm_kernel, dim3((unsigned)(tm * tn)), dim3(NTHREADS), 0, stream, g);
+  return hipGetLastError();
+}
+
+}  // namespace mlg

@@ -118,6 +118,52 @@ def bf16_narrow(x):
     return out
 
 
+def int8_quantize(x):
+    """(codes int8, exponents int32) of a float32 (rows, cols) tensor, profile int8i32.v1
+    (the reference's quantize_rows_int8_device, gemm/linalg_native.mojo:323-357)."""
+    _check(x, "x", torch.float32)
+    if x.dim() != 2 or x.numel() == 0:
+        raise ValueError("x must be 2-D and non-empty")
+    rows, cols = x.shape
+    codes = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    exps = torch.empty((rows,), dtype=torch.int32, device=x.device)
+    with torch.cuda.device(x.device):
+        _native.check(_native.lib().mlg_int8_quantize(codes.data_ptr(), exps.data_ptr(), x.data_ptr(), rows, cols,
+                                                      _stream(x)))
+    return codes, exps
+
+
+def int8_dequantize(codes, exps):
+    """float32 ftz(code * 2^exps[row]) (dequantize_rows_int8_device, :359-393)."""
+    _check(codes, "codes", torch.int8)
+    _check(exps, "exponents", torch.int32)
+    if codes.dim() != 2 or codes.numel() == 0 or exps.numel() != codes.shape[0]:
+        raise ValueError("codes must be 2-D and non-empty with one exponent per row")
+    rows, cols = codes.shape
+    out = torch.empty((rows, cols), dtype=torch.float32, device=codes.device)
+    with torch.cuda.device(codes.device):
+        _native.check(_native.lib().mlg_int8_dequantize(out.data_ptr(), codes.data_ptr(), exps.data_ptr(), rows,
+                                                        cols, _stream(codes)))
+    return out
+
+
+def gemm_int8i32(qa, ea, qb, eb, *, out=None):
+    """C = qa . qb^T scaled by 2^(ea[i] + eb[j]) (profile int8i32.v1, OP_NT; the reference's
+    identical_gemm_int8_into, gemm/linalg_native.mojo:258-321)."""
+    _check(qa, "qa", torch.int8)
+    _check(qb, "qb", torch.int8)
+    _check(ea, "ea", torch.int32)
+    _check(eb, "eb", torch.int32)
+    m, n, k = _shape(qa, qb, OP_NT)
+    if ea.numel() != m or eb.numel() != n:
+        raise ValueError("one exponent per row of each operand is required")
+    c = _prep_out(out, m, n, qa)
+    with torch.cuda.device(qa.device):
+        _native.check(_native.lib().mlg_gemm_int8i32(c.data_ptr(), qa.data_ptr(), ea.data_ptr(), qb.data_ptr(),
+                                                     eb.data_ptr(), m, n, k, _stream(qa)))
+    return c
+
+
 T_F32, T_BF16, T_I8 = 0, 1, 2
 
 

@@ -22,12 +22,18 @@ PROFILE_BF16 = f"mojolearn.identical.gemm.bf16f32.v{LOWBIT_PROFILE_VERSION}"
 #: This build's int8-weight extension: int8 codes times one float32 scale per output
 #: column, dequantized exactly as ftz(f32(code) * ftz(scale)) and then fp32.v1.
 PROFILE_INT8W = "mojolearn.identical.gemm.int8w-colscale-f32.v1"
+PROFILE_INT8 = f"mojolearn.identical.gemm.int8i32.v{LOWBIT_PROFILE_VERSION}"
+#: Contract L-7: the Int32 sum of k products of codes in [-127, 127] stays exact.
+INT8_MAX_K = 131072
 
 OP_NN, OP_NT, OP_TN = 0, 1, 2
 
 # op codes of the native table (gemm/linalg_dispatch.mojo:14-75, + this build's 15, 16)
 _LIN_OP_GEMM = 0
 _LIN_OP_GEMM_BF16 = 1
+_LIN_OP_GEMM_INT8 = 2
+_LIN_OP_QUANTIZE_INT8 = 3
+_LIN_OP_DEQUANTIZE_INT8 = 4
 _LIN_OP_TO_BF16 = 8
 _LIN_OP_FROM_BF16 = 9
 _LIN_OP_MODE = 11
@@ -289,6 +295,100 @@ def matmul_int8w(a, codes, scales, *, transpose_b=False, out=None):
     return C
 
 
+_RESHAPE_HINT = ("Reshape your data either using array.reshape(-1, 1) if your data has a single feature or "
+                 "array.reshape(1, -1) if it contains a single sample.")
+
+
+def _typed(x, dtype, ndim, name):
+    """`admit_typed` (bindings/admitted_input_unpack.mojo:1198-1233): `x` as C-order words of
+    `dtype` and rank `ndim`, converted by astype's rules when it has another numeric dtype,
+    refused when empty."""
+    v = _asarray(x)
+    if v.dtype.kind not in "biuf":
+        raise TypeError(f"mojolearn: {name} has buffer format '{v.dtype.str}', which is not a numeric array")
+    if v.ndim != ndim:
+        hint = ". " + _RESHAPE_HINT if ndim == 2 and v.ndim < 2 else ""
+        raise ValueError(f"mojolearn: {name} must be {ndim}-D, got {v.ndim}-D shape {_shape_text(v.shape)}{hint}")
+    if v.size == 0:
+        what = "feature(s)" if v.ndim == 2 and v.shape[0] != 0 else "sample(s)"
+        shape = _shape_text(v.shape)
+        raise ValueError(f"mojolearn: {name} is empty, shape {shape}: Found array with 0 {what} (shape={shape}) "
+                         "while a minimum of 1 is required.")
+    return np.ascontiguousarray(v, dtype=dtype)
+
+
+def _quantize(A):
+    """`lin_quantize_int8` (bindings/linalg_ops_lowbit_door.mojo:565-575) of an admitted operand."""
+    rows, cols = A.shape
+    codes = np.empty((rows, cols), dtype=np.int8)
+    exps = np.empty((rows,), dtype=np.int32)
+    _native.call(_LIN_OP_QUANTIZE_INT8, [codes.ctypes.data, exps.ctypes.data, A.ctypes.data], [rows, cols])
+    return codes, exps
+
+
+def quantize_int8(x):
+    """Quantize a 2-D float32 matrix to int8 codes with one power-of-two exponent per row
+    (profile ``mojolearn.identical.gemm.int8i32.v1``, contract L-3 and L-4).
+
+    Per row ``e = floor(log2(max |x|)) - 6`` (0 for an all-zero row) and
+    ``code = clamp(round_half_even(ftz(x) * 2**-e), -127, 127)``, a NaN coding to 0.
+    Returns ``(codes, exponents)``: int8 of `x`'s shape and int32 of shape (rows,), so that
+    ``row ~= codes * 2**exponent``.  python/mojolearn/_linalg_impl.py:330-340.
+    """
+    require_identical()
+    return _quantize(_operand(x, "x"))
+
+
+def dequantize_int8(codes, exponents):
+    """float32 ``codes * 2**exponents[row]`` exactly (contract L-6) from `quantize_int8` output.
+    bindings/linalg_ops_lowbit_door.mojo:585-601."""
+    require_identical()
+    Q = _typed(codes, np.int8, 2, "codes")
+    E = _typed(exponents, np.int32, 1, "exponents")
+    rows, cols = Q.shape
+    if E.shape[0] != rows:
+        raise ValueError(f"mojolearn.linalg.dequantize_int8: exponents has shape {_shape_text(E.shape)}, "
+                         f"want ({rows},)")
+    out = np.empty((rows, cols), dtype=np.float32)
+    _native.call(_LIN_OP_DEQUANTIZE_INT8, [out.ctypes.data, Q.ctypes.data, E.ctypes.data], [rows, cols])
+    return out
+
+
+def _int8_operand(x, name):
+    """`_lin_int8_operand` (door :604-620): a (codes, exponents) pair, or a float32 matrix
+    quantized by `quantize_int8`'s rule."""
+    if type(x) is tuple and len(x) == 2:
+        Q = _typed(x[0], np.int8, 2, name + " codes")
+        E = _typed(x[1], np.int32, 1, name + " exponents")
+        if E.shape[0] != Q.shape[0]:
+            raise ValueError(f"mojolearn.linalg.matmul_int8: {name} exponents has shape {_shape_text(E.shape)}, "
+                             f"want ({Q.shape[0]},)")
+        return Q, E
+    return _quantize(_operand(x, name))
+
+
+def matmul_int8(a, b, *, out=None):
+    """``a @ b.T`` with int8 operands under ``mojolearn.identical.gemm.int8i32.v1`` (OP_NT only).
+
+    Each of `a` (m, k) and `b` (n, k) is a float32 matrix, quantized by `quantize_int8`'s
+    rule, or a ``(codes, exponents)`` pair.  ``C[i, j] = ftz(f32(sum_p qa[i, p] qb[j, p]) *
+    2**(ea[i] + eb[j]))``: the exact Int32 sum, converted by the contract's pinned split
+    (L-5), scaled once.  It is the product of the rounded operands, not the float32
+    product.  python/mojolearn/_linalg_impl.py:360-369, door :623-650.
+    """
+    require_identical()
+    qa, ea = _int8_operand(a, "a")
+    qb, eb = _int8_operand(b, "b")
+    m, k = qa.shape
+    n, kb = qb.shape
+    if k != kb:
+        raise ValueError(f"mojolearn.linalg.matmul_int8: contracted extents differ, a gives k={k} and b gives k={kb}")
+    C = _out(out, m, n, "matmul_int8")
+    _native.call(_LIN_OP_GEMM_INT8, [C.ctypes.data, qa.ctypes.data, ea.ctypes.data, qb.ctypes.data, eb.ctypes.data],
+                 [m, n, k])
+    return C
+
+
 def linear(x, w, bias, *, transpose_b=False, out=None):
     """``Y = ftz(ftz(x @ w) + ftz(bias[j]))``: the product, then the LM's nn.Linear bias
     (transformer/impl/llama/modeling_llama.mojo:3979-3989), fused into the store."""
@@ -306,6 +406,7 @@ def linear(x, w, bias, *, transpose_b=False, out=None):
     return C
 
 
-__all__ = ["matmul", "matmul_bf16", "matmul_int8w", "linear", "to_bf16", "from_bf16", "numeric_mode",
-           "profile", "require_identical", "PROFILE", "PROFILE_FAMILY", "PROFILE_VERSION", "PROFILE_BF16",
-           "PROFILE_INT8W", "OP_NN", "OP_NT", "OP_TN"]
+__all__ = ["matmul", "matmul_bf16", "matmul_int8", "matmul_int8w", "linear", "to_bf16", "from_bf16",
+           "quantize_int8", "dequantize_int8", "numeric_mode", "profile", "require_identical", "PROFILE",
+           "PROFILE_FAMILY", "PROFILE_VERSION", "PROFILE_BF16", "PROFILE_INT8", "PROFILE_INT8W", "INT8_MAX_K",
+           "OP_NN", "OP_NT", "OP_TN"]

@@ -17,6 +17,7 @@
  *   - NaN canonicalization      core/nan_canon.mojo:55-130
  *   - bias add                  transformer/impl/llama/modeling_llama.mojo:3979-3989
  *   - card fill + FNV-1a64      bench/gemm_card_main.mojo:292-311, core/identity_trace.mojo:89-115
+ *   - int8i32.v1 (L-3..L-7)     checks/numerics.mojo:1577-1677, gemm/host/gemm_lowbit_oracle.mojo:171-251
  * and a fast threaded arm that computes the same bits (the role of the reference's
  * gemm/host/gemm_host_rows.mojo:467-556): operands flushed once, columns vectorised
  * with AVX2 FMA (one independent chain per column, so no reassociation inside a leaf),
@@ -323,6 +324,100 @@ void orc_int8_dequant(float* out, const int8_t* codes, const float* scales, int6
 }
 
 /* core/identity_trace.mojo:89-115: FNV-1a64 over bytes in order. */
+/* ---- profile mojolearn.identical.gemm.int8i32.v1 (gemm/IDENTICAL_LOWBIT_CONTRACT.md L-3..L-7) ----
+ * Both operands are int8 codes with one power-of-two exponent per row; OP_NT only. */
+
+/* checks/numerics.mojo:1589-1598 pow2_f32: 2^e from the exponent field; above 127 the
+ * infinity, below -126 +0.0 (no subnormal scales). */
+static inline float pow2_f32(int64_t e) {
+  if (e > 127) return u2f(0x7F800000u);
+  if (e < -126) return 0.0f;
+  return u2f((uint32_t)(e + 127) << 23);
+}
+
+/* checks/numerics.mojo:1577-1586 f32_round_half_even: the magic-constant rounding. */
+static inline float round_half_even_f32(float x) {
+  const float magic = 12582912.0f;
+  if (x >= 0.0f) return (x + magic) - magic;
+  return (x - magic) + magic;
+}
+
+/* checks/numerics.mojo:1609-1630 i32_to_f32_pinned (L-5): a 20-bit high part and a 12-bit
+ * low part converted exactly, the high part scaled by 2^12 exactly, one IEEE addition. */
+float orc_q8_i32_to_f32(int32_t v) {
+  const int neg = v < 0;
+  int64_t w = v;
+  if (neg) w = -w;
+  const uint32_t mag = (uint32_t)w;
+  const float hi = (float)(mag >> 12);
+  const float lo = (float)(mag & 0xFFFu);
+  const float r = hi * 4096.0f + lo;
+  return neg ? -r : r;
+}
+
+/* checks/numerics.mojo:1638-1647 int8_row_exponent (L-3): floor(log2 absmax) - 6 read off the
+ * exponent field (checks/numerics.mojo:1601-1606); a zero row takes 0. */
+int orc_q8_row_exponent(float absmax) {
+  const float a = ftz(absmax);
+  if (a == 0.0f || a != a) return 0;
+  return (int)((f2u(a) >> 23) & 0xFFu) - 127 - 6;
+}
+
+/* checks/numerics.mojo:1650-1668 quantize_int8_value (L-4). */
+static inline int8_t q8_value(float x, int e) {
+  if (x != x) return 0;
+  const float s = ftz(ftz(x) * pow2_f32(-(int64_t)e));
+  float r = round_half_even_f32(s);
+  /* A zero times an infinite 2^-e (a row whose absmax is below 2^-121) is NaN; the
+   * reference's Int8(Int(NaN)) keeps the low byte of the integer-indefinite word, 0. */
+  if (r != r) return 0;
+  if (r > 127.0f) r = 127.0f;
+  if (r < -127.0f) r = -127.0f;
+  return (int8_t)(int)r;
+}
+
+/* gemm/host/gemm_lowbit_oracle.mojo:171-198 row_absmax + quantize_rows_int8: per row the
+ * largest flushed magnitude (a NaN never wins the comparison), its exponent, the codes. */
+void orc_q8_quantize_rows(int8_t* codes, int32_t* exps, const float* x, int64_t rows, int64_t cols) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    float best = 0.0f;
+    for (int64_t c = 0; c < cols; ++c) {
+      float v = ftz(x[r * cols + c]);
+      if (v < 0.0f) v = -v;
+      if (v > best) best = v;
+    }
+    const int e = orc_q8_row_exponent(best);
+    exps[r] = e;
+    for (int64_t c = 0; c < cols; ++c) codes[r * cols + c] = q8_value(x[r * cols + c], e);
+  }
+}
+
+/* checks/numerics.mojo:1671-1677 dequant_int8_pinned (L-6) on an Int32 and an exponent sum. */
+static inline float q8_dequant(int32_t acc, int64_t e_sum) {
+  return ftz(orc_q8_i32_to_f32(acc) * pow2_f32(e_sum));
+}
+
+/* gemm/host/gemm_lowbit_oracle.mojo:201-214 dequantize_rows_int8: code * 2^e per row. */
+void orc_q8_dequantize_rows(float* out, const int8_t* codes, const int32_t* exps, int64_t rows, int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) out[r * cols + c] = q8_dequant(codes[r * cols + c], exps[r]);
+}
+
+/* gemm/host/gemm_lowbit_oracle.mojo:217-251 int8_dot_cell + gemm_int8_oracle (L-7): OP_NT,
+ * C[i,j] = ftz(f32(sum_p qa[i,p] qb[j,p]) * 2^(ea[i] + eb[j])), the sum exact in Int32 for
+ * k <= 131072. */
+void orc_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb, int64_t m,
+                 int64_t n, int64_t k) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      int32_t acc = 0;
+      for (int64_t p = 0; p < k; ++p) acc += (int32_t)qa[i * k + p] * (int32_t)qb[j * k + p];
+      c[i * n + j] = q8_dequant(acc, (int64_t)ea[i] + (int64_t)eb[j]);
+    }
+}
+
 uint64_t orc_fnv1a64(const void* data, int64_t nbytes) {
   const uint8_t* p = (const uint8_t*)data;
   uint64_t h = 0xCBF29CE484222325ull;

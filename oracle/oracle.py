@@ -44,6 +44,11 @@ def lib():
         L.orc_bf16_narrow.argtypes = [vp, vp, i64]; L.orc_bf16_narrow.restype = None
         L.orc_int8_dequant.argtypes = [vp, vp, vp, i64, i64, c_int]; L.orc_int8_dequant.restype = None
         L.orc_fnv1a64.argtypes = [vp, i64]; L.orc_fnv1a64.restype = ctypes.c_uint64
+        L.orc_q8_i32_to_f32.argtypes = [ctypes.c_int32]; L.orc_q8_i32_to_f32.restype = f32
+        L.orc_q8_row_exponent.argtypes = [f32]; L.orc_q8_row_exponent.restype = c_int
+        L.orc_q8_quantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_quantize_rows.restype = None
+        L.orc_q8_dequantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_dequantize_rows.restype = None
+        L.orc_q8_gemm.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q8_gemm.restype = None
         L.orc_card_fill.argtypes = [vp, i64, i64]; L.orc_card_fill.restype = None
         L.orc_ftz.argtypes = [f32]; L.orc_ftz.restype = f32
         L.orc_fma.argtypes = [f32, f32, f32]; L.orc_fma.restype = f32
@@ -177,3 +182,49 @@ def ftz(x):
 
 def max_threads():
     return lib().orc_max_threads()
+
+
+# ---- profile mojolearn.identical.gemm.int8i32.v1 (gemm/IDENTICAL_LOWBIT_CONTRACT.md L-3..L-7)
+
+INT8_MAX_K = 131072
+
+
+def q8_quantize(x):
+    """Per-row power-of-two exponent and int8 codes (L-3, L-4): (codes int8, exponents int32)."""
+    x = _f32c(x)
+    rows, cols = x.shape
+    codes = np.empty((rows, cols), np.int8)
+    exps = np.empty(rows, np.int32)
+    lib().orc_q8_quantize_rows(_p(codes), _p(exps), _p(x), rows, cols)
+    return codes, exps
+
+
+def q8_dequantize(codes, exps):
+    """codes * 2^exponent per row, the pinned dequantization (L-5, L-6)."""
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    exps = np.ascontiguousarray(exps, dtype=np.int32)
+    rows, cols = codes.shape
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_q8_dequantize_rows(_p(out), _p(codes), _p(exps), rows, cols)
+    return out
+
+
+def q8_gemm(qa, ea, qb, eb):
+    """C = qa . qb^T (OP_NT) as int8i32.v1: the exact Int32 sum, pinned to float32, scaled."""
+    qa = np.ascontiguousarray(qa, dtype=np.int8)
+    qb = np.ascontiguousarray(qb, dtype=np.int8)
+    ea = np.ascontiguousarray(ea, dtype=np.int32)
+    eb = np.ascontiguousarray(eb, dtype=np.int32)
+    (m, k), (n, kb) = qa.shape, qb.shape
+    assert k == kb and ea.size == m and eb.size == n
+    c = np.empty((m, n), np.float32)
+    lib().orc_q8_gemm(_p(c), _p(qa), _p(ea), _p(qb), _p(eb), m, n, k)
+    return c
+
+
+def q8_i32_to_f32(v):
+    return lib().orc_q8_i32_to_f32(int(v))
+
+
+def q8_row_exponent(absmax):
+    return lib().orc_q8_row_exponent(float(absmax))

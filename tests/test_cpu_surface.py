@@ -65,7 +65,19 @@ def test_op_table_errors_come_through_the_sink_once():
     with pytest.raises(RuntimeError, match="must all be positive"):
         _native.call(0, [1, 2, 3], [0, 1, 1, 0])
     with pytest.raises(RuntimeError, match="not part of this build"):
-        _native.call(2, [1, 2, 3, 4, 5], [1, 1, 1])
+        _native.call(5, [1, 2, 3, 4, 5, 6, 7], [1, 1, 1])
+    with pytest.raises(RuntimeError, match="invalid gemm_int8 address count"):
+        _native.call(2, [1, 2, 3, 4], [1, 1, 1])
+    with pytest.raises(RuntimeError, match=r"gemm_int8: params must contain 3 values \(m, n, k\), got 4"):
+        _native.call(2, [1, 2, 3, 4, 5], [1, 1, 1, 1])
+    with pytest.raises(RuntimeError, match="gemm_int8: m, n and k must all be positive, got m=1 n=1 k=0"):
+        _native.call(2, [1, 2, 3, 4, 5], [1, 1, 0])
+    with pytest.raises(RuntimeError, match=r"gemm_int8: k must be at most 131072 \(contract L-7\), got 131073"):
+        _native.call(2, [1, 2, 3, 4, 5], [1, 1, 131073])
+    with pytest.raises(RuntimeError, match="quantize_int8: rows and cols must be positive, got 0 x 3"):
+        _native.call(3, [1, 2, 3], [0, 3])
+    with pytest.raises(RuntimeError, match=r"dequantize_int8: params must contain 2 values \(rows, cols\), got 3"):
+        _native.call(4, [1, 2, 3], [1, 2, 3])
     L = _native.lib()
     msgs = []
     sink = _native.SINK_T(lambda ctx, p, n: msgs.append((ctx, ctypes.string_at(p, n))))

@@ -68,3 +68,5 @@ def test_verify_gemm_lanes(oracle, kind):
     assert VL.train_hash(VL.lane_gemm_pinned(S.matmul, X)) == cells[f"gemm-pinned/{kind}"]["train"]
     assert VL.train_hash(VL.lane_gemm_transposed(S.matmul, X)) == cells[f"gemm-transposed/{kind}"]["train"]
     assert VL.train_hash(VL.lane_gemm_bf16(S.to_bf16, S.matmul_bf16, X)) == cells[f"gemm-bf16/{kind}"]["train"]
+    lane = VL.lane_gemm_int8(S.quantize_int8, S.matmul_int8, S.dequantize_int8, X)
+    assert VL.train_hash(lane) == cells[f"gemm-int8/{kind}"]["train"]

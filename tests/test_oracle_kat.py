@@ -136,3 +136,133 @@ def test_nan_canon(oracle):
                  np.uint32)
     got = oracle.nan_canon(w.view(np.float32)).view(np.uint32)
     assert list(got) == [0x7FC00000, 0x7FC00000, 0x7FC00000, 0x7F800000, 0xFF800000, 0x00000001, 0x80000000]
+
+
+# ---- int8i32.v1 (gemm/IDENTICAL_LOWBIT_CONTRACT.md L-3..L-7), pinned by independent arithmetic:
+# exact rationals, numpy's own int->float rounding and ldexp, not the oracle's spelling.
+
+def _ftz32(v):
+    v = np.asarray(v, np.float32).copy()
+    u = v.view(np.uint32)
+    sub = ((u & 0x7F800000) == 0) & ((u & 0x007FFFFF) != 0)
+    u[sub] &= 0x80000000
+    return v
+
+
+def test_int8_i32_to_f32_is_round_half_even(oracle):
+    """L-5: the split conversion equals one round-to-nearest-even of the integer, which is
+    numpy's int64 -> float32 cast; ties at 2^24..2^31 included."""
+    rng = np.random.default_rng(5)
+    vals = list(rng.integers(-(2 ** 31) + 1, 2 ** 31, 4000))
+    for p in range(23, 31):
+        for d in (-3, -2, -1, 0, 1, 2, 3):
+            vals += [2 ** p + d, -(2 ** p) - d, 2 ** p + 2 ** (p - 23) + d]
+    vals += [0, 1, -1, 2 ** 31 - 1, -(2 ** 31) + 1, 16129 * 131072, -16129 * 131072]
+    for v in vals:
+        want = np.array([v], np.int64).astype(np.float32)[0]
+        got = np.float32(oracle.q8_i32_to_f32(int(v)))
+        assert got.view(np.uint32) == want.view(np.uint32), v
+
+
+def test_int8_row_exponent(oracle):
+    """L-3: floor(log2 absmax) - 6, by frexp; a zero, subnormal or NaN absmax gives 0."""
+    rng = np.random.default_rng(6)
+    xs = np.concatenate([np.exp2(np.arange(-126, 128)).astype(np.float32),
+                         (rng.uniform(0.5, 1.0, 500) * np.exp2(rng.integers(-125, 128, 500))).astype(np.float32)])
+    xs = np.concatenate([xs, np.nextafter(xs, np.float32(0))])
+    for x in xs:
+        if x < np.finfo(np.float32).tiny:
+            continue
+        _, e2 = np.frexp(np.float64(x))
+        assert oracle.q8_row_exponent(x) == int(e2) - 1 - 6, x
+    sub = np.array([0x00000001, 0x007FFFFF], np.uint32).view(np.float32)
+    for x in [np.float32(0.0), sub[0], sub[1], np.float32(np.nan)]:
+        assert oracle.q8_row_exponent(x) == 0
+    assert oracle.q8_row_exponent(np.float32(np.inf)) == 255 - 127 - 6
+
+
+def test_int8_quantize_rule(oracle):
+    """L-4: codes = clamp(round_half_even(x * 2^-e), -127, 127) by exact rationals, with rows
+    built to hold exact ties, the 127.5 -> 128 -> 127 clamp, subnormals and a zero row."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    rows = []
+    for r in range(40):
+        scale = 2.0 ** int(rng.integers(-110, 110))
+        halves = rng.integers(-255, 256, 64).astype(np.float64) / 2.0  # ties at every .5
+        row = halves * scale / 2 ** 6
+        row[0] = 127.75 * scale / 2 ** 6 * (1 if r % 2 else -1)  # absmax in [64, 128) after scaling
+        rows.append(row)
+    rows.append(rng.standard_normal(64) * 3.0)
+    x = np.array(rows, np.float32)
+    x[-1, 5] = np.array([0x00000005], np.uint32).view(np.float32)[0]  # flushed to zero
+    x = np.concatenate([x, np.zeros((1, 64), np.float32)])
+    codes, exps = oracle.q8_quantize(x)
+    fx = _ftz32(x)
+    for i in range(x.shape[0]):
+        absmax = np.max(np.abs(fx[i].astype(np.float64)))
+        e = 0 if absmax == 0 else int(np.frexp(absmax)[1]) - 1 - 6
+        assert exps[i] == e
+        for j in range(x.shape[1]):
+            s = Fraction(float(fx[i, j])) * (Fraction(2) ** -e)
+            q = max(-127, min(127, round(s)))  # Fraction.__round__ is half-to-even
+            assert codes[i, j] == q, (i, j, float(x[i, j]), e)
+    assert (codes[-1] == 0).all() and exps[-1] == 0
+
+
+def test_int8_quantize_specials(oracle):
+    """NaN codes to 0 and never wins the absmax; an infinity codes to +-127; a row whose
+    absmax is below 2^-121 has an infinite 2^-e: nonzero entries clamp, zeros code to 0."""
+    x = np.array([[np.nan, 1.0, -0.5, 0.25],
+                  [np.inf, 1.0, -np.inf, 0.0],
+                  [2.0 ** -124, -(2.0 ** -125), 0.0, -0.0]], np.float32)
+    codes, exps = oracle.q8_quantize(x)
+    assert list(exps) == [-6, 122, -130]
+    assert list(codes[0]) == [0, 64, -32, 16]
+    assert list(codes[1]) == [127, 0, -127, 0]
+    assert list(codes[2]) == [127, -127, 0, 0]
+
+
+def test_int8_dequantize_rule(oracle):
+    """L-6: code * 2^e exactly (ldexp), flushed below the normal range; 2^e is infinite above
+    127 (so a zero code gives NaN, canonical on the surface) and +0 below -126."""
+    rng = np.random.default_rng(8)
+    codes = rng.integers(-127, 128, (6, 50)).astype(np.int8)
+    codes[:, 0] = 0
+    exps = np.array([-140, -133, -20, 0, 100, 121], np.int32)
+    got = oracle.q8_dequantize(codes, exps)
+    want = _ftz32(np.ldexp(codes.astype(np.float64), exps[:, None].astype(np.int64)).astype(np.float32))
+    want[0] = np.where(codes[0] < 0, np.float32(-0.0), np.float32(0.0))  # 2^-140 is +0, sign of code
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    big = oracle.nan_canon(oracle.q8_dequantize(np.array([[0, 3, -3]], np.int8), np.array([128], np.int32)))
+    assert list(big.view(np.uint32).ravel()) == [0x7FC00000, 0x7F800000, 0xFF800000]
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 5, 1), (7, 4, 33), (5, 9, 300), (2, 3, 4097)])
+def test_int8_gemm_exact(oracle, m, n, k):
+    """L-7: the exact integer dot (numpy int64 matmul) rounded once to float32 and scaled by
+    an exact power of two, flushed; exponent sums reach the overflow and underflow edges."""
+    rng = np.random.default_rng(m * 1000 + k)
+    qa = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qb = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    ea = rng.integers(-70, 70, m).astype(np.int32)
+    eb = rng.integers(-70, 70, n).astype(np.int32)
+    ea[0], eb[0] = -140, 10
+    got = oracle.q8_gemm(qa, ea, qb, eb)
+    acc = qa.astype(np.int64) @ qb.astype(np.int64).T
+    f = acc.astype(np.float32).astype(np.float64)
+    es = ea[:, None].astype(np.int64) + eb[None, :].astype(np.int64)
+    want = _ftz32(np.where(es < -126, f * 0.0, np.ldexp(f, es)).astype(np.float32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_int8_gemm_at_max_k(oracle):
+    """k = 131072 with every code at +-127: |sum| = 16129 * 2^17 < 2^31, no wrap, one rounding."""
+    k = 131072
+    qa = np.full((2, k), 127, np.int8)
+    qa[1, ::2] = -127
+    qb = np.full((2, k), 127, np.int8)
+    e0 = np.zeros(2, np.int32)
+    got = oracle.q8_gemm(qa, e0, qb, e0)
+    full = np.array([16129 * k], np.int64).astype(np.float32)[0]
+    assert got[0, 0] == full and got[0, 1] == full and got[1, 0] == 0.0

@@ -2,7 +2,7 @@
 
 Fixtures: tools/identity_break.py:1393 (N, D = 20000, 16) and :1414-1485 (`fixture`,
 `_hashed_uniform`).  Hashes: `_h` / `_train_hash` (:1355-1382).  Lanes: gemm-pinned
-(:2984-2995), gemm-transposed (:5880-5890), gemm-bf16 (:3825-3836).  The recorded
+(:2984-2995), gemm-transposed (:5880-5890), gemm-bf16 (:3825-3836), gemm-int8 (:3839-3849).  The recorded
 `train` hashes are in tests/golden/verify_gemm_cells.json (from
 python/mojolearn/verify_reference/table.json).
 
@@ -115,6 +115,18 @@ def lane_gemm_bf16(to_bf16, matmul_bf16, X):
     return dict(nt=h(c1), both=h(c2), nn=h(c3), bits=h(bb))
 
 
+def lane_gemm_int8(quantize_int8, matmul_int8, dequantize_int8, X):
+    """int8i32.v1 on fixture slices: the quantizer's codes and exponents, the product of
+    the two quantized operands (a . b^T) and a dequantization."""
+    a = np.ascontiguousarray(X[:256]).astype(np.float32)
+    b = np.ascontiguousarray(X[256:256 + 128]).astype(np.float32)
+    qa, ea = quantize_int8(a)
+    qb, eb = quantize_int8(b)
+    c = matmul_int8((qa, ea), (qb, eb))
+    return dict(codes=h(np.asarray(qa), np.asarray(qb)), exps=h(np.asarray(ea), np.asarray(eb)),
+                product=h(np.asarray(c)), dequant=h(np.asarray(dequantize_int8(qb, eb))))
+
+
 class OracleSurface:
     """The three surface calls the lanes need, answered by the CPU oracle."""
 
@@ -132,3 +144,14 @@ class OracleSurface:
         a = np.asarray(a)
         af = self.O.bf16_widen(a) if a.dtype == np.uint16 else a
         return self.matmul(af, self.O.bf16_widen(b), transpose_a, transpose_b)
+
+    def quantize_int8(self, x):
+        return self.O.q8_quantize(x)
+
+    def dequantize_int8(self, codes, exps):
+        return self.O.nan_canon(self.O.q8_dequantize(codes, exps))
+
+    def matmul_int8(self, a, b):
+        qa, ea = a if isinstance(a, tuple) else self.O.q8_quantize(a)
+        qb, eb = b if isinstance(b, tuple) else self.O.q8_quantize(b)
+        return self.O.nan_canon(self.O.q8_gemm(qa, ea, qb, eb))
