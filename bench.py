@@ -78,6 +78,8 @@ def profiled_traffic(path=PREFILL_PROFILE):
 
 
 def _rows(m, count=8):
+    if m <= count:
+        return np.arange(m)
     return np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m).choice(m, count - 2, replace=False)]))
 
 
@@ -203,6 +205,66 @@ def bench_compare(torch, D, steps, warmup):
     return out
 
 
+#: The reference's int8i32.v1 rows on MI325X (its integer-MMA arm, best ms of its runs;
+#: bench/results/lowbit_amd_tuned/2026-09-29/mi325x/*/lowbit.tsv).
+INT8I32_ROWS = [("qkv.t1", 1, 4096, 4096, 0.0480), ("qkv.t8", 8, 4096, 4096, 0.0496),
+                ("qkv.t512", 512, 4096, 4096, 0.2644), ("mlp_up.t1", 1, 14336, 4096, 0.0531),
+                ("mlp_up.t8", 8, 14336, 4096, 0.0609), ("mlp_up.t512", 512, 14336, 4096, 0.8768),
+                ("mlp_down.t1", 1, 4096, 14336, 0.1363), ("mlp_down.t8", 8, 4096, 14336, 0.1406),
+                ("mlp_down.t512", 512, 4096, 14336, 0.8387), ("lm_head.t1", 1, 128256, 4096, 0.2742),
+                ("lm_head.t8", 8, 128256, 4096, 0.3185), ("lm_head.t512", 512, 16032, 4096, 1.0085)]
+
+
+class Int8Call:
+    """One int8i32.v1 product C = qa . qb^T on device buffers, launched on a given stream."""
+
+    def __init__(self, torch, qa, ea, qb, eb):
+        from mojolearn_amd import _native
+        self.lib, self.check = _native.lib(), _native.check
+        self.qa, self.ea, self.qb, self.eb = qa, ea, qb, eb
+        self.m, self.k = qa.shape
+        self.n = qb.shape[0]
+        self.out = torch.empty((self.m, self.n), dtype=torch.float32, device=qa.device)
+        nb = self.lib.mlg_gemm_int8i32_workspace_bytes(qa.data_ptr(), qb.data_ptr(), self.m, self.n, self.k)
+        if nb < 0:
+            raise RuntimeError(self.lib.mlg_last_error().decode())
+        self.nb = nb
+        self.ws = torch.empty(max(nb, 4), dtype=torch.uint8, device=qa.device)
+
+    def __call__(self, stream=None):
+        import torch
+        s = stream if stream is not None else torch.cuda.current_stream()
+        self.check(self.lib.mlg_gemm_int8i32_ws(self.out.data_ptr(), self.qa.data_ptr(), self.ea.data_ptr(),
+                                                self.qb.data_ptr(), self.eb.data_ptr(), self.m, self.n, self.k,
+                                                self.ws.data_ptr(), self.nb, s.cuda_stream))
+
+
+def bench_int8i32(torch, O, steps, warmup, check):
+    """The int8i32.v1 product (integer MFMA) on the reference's Llama-8B rows: codes and row
+    exponents resident in HBM, the same buffers every call (as the reference measured them);
+    TOP/s counts 2mnk, and the weight codes' GB/s is reported for the skinny rows."""
+    rng = np.random.default_rng(11)
+    out = {}
+    for name, m, n, k, ref_ms in INT8I32_ROWS:
+        qa = rng.integers(-127, 128, (m, k), dtype=np.int8)
+        qb = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        ea = rng.integers(-20, 0, m).astype(np.int32)
+        eb = rng.integers(-20, 0, n).astype(np.int32)
+        call = Int8Call(torch, _t(torch, qa), _t(torch, ea), _t(torch, qb), _t(torch, eb))
+        ms = graph_time([call], steps, warmup, torch)
+        row = {"ms": ms, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12,
+               "weight_gbs": n * k / (ms * 1e-3) / 1e9, "reference_mi325x_ms": ref_ms,
+               "speedup_vs_reference": ref_ms / ms}
+        if check:
+            rows = _rows(m, 4)
+            want = O.nan_canon(O.q8_gemm(qa[rows], ea[rows], qb, eb))
+            row["mismatched_words"] = _mismatch(call.out.cpu().numpy()[rows], want)
+            row["checked_cells"] = int(len(rows) * n)
+        out[name] = row
+        del call
+    return out
+
+
 def copy_calibration(torch, nbytes=1 << 30):
     """Three copies of a 1 GiB float32 buffer (torch's elementwise copy kernel): each dispatch
     reads and writes exactly `nbytes`, the yardstick for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -266,6 +328,7 @@ def main():
 
     if args.compare:
         extra["compare"] = bench_compare(torch, D, args.steps, args.warmup)
+        extra["int8i32"] = bench_int8i32(torch, O, args.steps, args.warmup, check)
 
     line = {
         "metric": "identical-mode FP32 GEMM TFLOP/s & % of peak; GEMV GB/s; 0 mismatched bits",

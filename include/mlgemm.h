@@ -112,14 +112,20 @@ int mlg_bf16_narrow(uint16_t* out, const float* in, int64_t count, void* stream)
  *   clamp(rne(ftz(x) * 2^-e), -127, 127), a NaN coding to 0.
  * dequantize: out = ftz(code * 2^e) per row.
  * gemm: OP_NT, C[i][j] = ftz(f32(sum_p qa[i][p] qb[j][p]) * 2^(ea[i] + eb[j])) with the sum exact in
- *   Int32 and converted by the pinned split (L-5); 1 <= k <= 131072.  Allocates a repack buffer from
- *   the stream-ordered pool only when k is not a multiple of 16 or a base is not 16-byte aligned. */
+ *   Int32 and converted by the pinned split (L-5); 1 <= k <= 131072.  mlg_gemm_int8i32 takes its
+ *   workspace (a repack of operands whose k is not a multiple of 16 or whose base is not 16-byte
+ *   aligned; Int32 partial sums when k is split to fill the CUs) from the stream-ordered pool;
+ *   mlg_gemm_int8i32_ws takes it from the caller (mlg_gemm_int8i32_workspace_bytes bytes for
+ *   these operand addresses on the current device, -1 on error) and allocates nothing. */
 int mlg_int8_quantize(int8_t* codes, int32_t* exponents, const float* x, int64_t rows, int64_t cols,
                       void* stream);
 int mlg_int8_dequantize(float* out, const int8_t* codes, const int32_t* exponents, int64_t rows,
                         int64_t cols, void* stream);
 int mlg_gemm_int8i32(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
                      int64_t m, int64_t n, int64_t k, void* stream);
+int64_t mlg_gemm_int8i32_workspace_bytes(const int8_t* qa, const int8_t* qb, int64_t m, int64_t n, int64_t k);
+int mlg_gemm_int8i32_ws(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
+                        int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* The message of the calling thread's last failed mlg_* call ("" if none). */
 const char* mlg_last_error(void);

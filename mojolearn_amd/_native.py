@@ -53,6 +53,10 @@ def lib():
         L.mlg_int8_dequantize.restype = ctypes.c_int
         L.mlg_gemm_int8i32.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, vp]
         L.mlg_gemm_int8i32.restype = ctypes.c_int
+        L.mlg_gemm_int8i32_workspace_bytes.argtypes = [vp, vp, i64, i64, i64]
+        L.mlg_gemm_int8i32_workspace_bytes.restype = i64
+        L.mlg_gemm_int8i32_ws.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp]
+        L.mlg_gemm_int8i32_ws.restype = ctypes.c_int
         L.mlg_last_error.argtypes = []
         L.mlg_last_error.restype = ctypes.c_char_p
         for name in ("mlg_numeric_mode", "mlg_profile_version", "mlg_lowbit_profile_version"):

@@ -278,9 +278,10 @@ int64_t host_q8_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>&
   up(dea, (const void*)ad[2], (size_t)m * 4, P.stream);
   up(dqb, (const void*)ad[3], (size_t)(n * k), P.stream);
   up(deb, (const void*)ad[4], (size_t)n * 4, P.stream);
-  const int64_t wsb = mlg::q8_workspace_bytes(dqa, dqb, m, n, k);
+  const int cus = num_cus_of_current_device();
+  const int64_t wsb = mlg::q8_workspace_bytes(dqa, dqb, m, n, k, cus);
   void* dws = wsb > 0 ? P.w.get((size_t)wsb) : nullptr;
-  hip_check(mlg::run_q8_gemm(dc, dqa, dea, dqb, deb, m, n, k, dws, num_cus_of_current_device(), P.stream),
+  hip_check(mlg::run_q8_gemm(dc, dqa, dea, dqb, deb, m, n, k, dws, cus, P.stream),
             "gemm_int8 launch");
   down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
   hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
@@ -477,26 +478,56 @@ int mlg_int8_dequantize(float* out, const int8_t* codes, const int32_t* exponent
   });
 }
 
+static void check_q8_args(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
+                          int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0)
+    throw Fail("gemm_int8: m, n and k must all be positive, got m=" + std::to_string(m) + " n=" +
+               std::to_string(n) + " k=" + std::to_string(k));
+  if (k > mlg::INT8_MAX_K)
+    throw Fail("gemm_int8: k must be at most " + std::to_string(mlg::INT8_MAX_K) + " (contract L-7), got " +
+               std::to_string(k));
+  if (!c || !ea || !eb || !qa || !qb) throw Fail("gemm_int8: null operand pointer");
+}
+
 int mlg_gemm_int8i32(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
                      int64_t m, int64_t n, int64_t k, void* stream) {
   return guarded([&] {
-    if (m <= 0 || n <= 0 || k <= 0)
-      throw Fail("gemm_int8: m, n and k must all be positive, got m=" + std::to_string(m) + " n=" +
-                 std::to_string(n) + " k=" + std::to_string(k));
-    if (k > mlg::INT8_MAX_K)
-      throw Fail("gemm_int8: k must be at most " + std::to_string(mlg::INT8_MAX_K) + " (contract L-7), got " +
-                 std::to_string(k));
-    if (!c || !ea || !eb || !qa || !qb) throw Fail("gemm_int8: null operand pointer");
+    check_q8_args(c, qa, ea, qb, eb, m, n, k);
     hipStream_t s = (hipStream_t)stream;
-    const int64_t wsb = mlg::q8_workspace_bytes(qa, qb, m, n, k);
+    const int cus = num_cus_of_current_device();
+    const int64_t wsb = mlg::q8_workspace_bytes(qa, qb, m, n, k, cus);
     void* ws = nullptr;
     if (wsb > 0) hip_check(hipMallocAsync(&ws, (size_t)wsb, s), "hipMallocAsync");
-    hipError_t e = mlg::run_q8_gemm(c, qa, ea, qb, eb, m, n, k, ws, num_cus_of_current_device(), s);
+    hipError_t e = mlg::run_q8_gemm(c, qa, ea, qb, eb, m, n, k, ws, cus, s);
     if (ws) {
       hipError_t f = hipFreeAsync(ws, s);
       if (e == hipSuccess) e = f;
     }
     hip_check(e, "gemm_int8 launch");
+  });
+}
+
+int64_t mlg_gemm_int8i32_workspace_bytes(const int8_t* qa, const int8_t* qb, int64_t m, int64_t n, int64_t k) {
+  int64_t r = -1;
+  const int rc = guarded([&] {
+    if (m <= 0 || n <= 0 || k <= 0 || k > mlg::INT8_MAX_K) throw Fail("gemm_int8: invalid shape");
+    r = mlg::q8_workspace_bytes(qa, qb, m, n, k, num_cus_of_current_device());
+  });
+  return rc == 0 ? r : -1;
+}
+
+int mlg_gemm_int8i32_ws(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
+                        int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    check_q8_args(c, qa, ea, qb, eb, m, n, k);
+    const int cus = num_cus_of_current_device();
+    const int64_t need = mlg::q8_workspace_bytes(qa, qb, m, n, k, cus);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      throw Fail("gemm_int8: workspace of " + std::to_string(workspace_bytes) + " bytes, this product needs " +
+                 std::to_string(need));
+    hip_check(mlg::run_q8_gemm(c, qa, ea, qb, eb, m, n, k, need > 0 ? workspace : nullptr, cus,
+                               (hipStream_t)stream),
+              "gemm_int8 launch");
   });
 }
 

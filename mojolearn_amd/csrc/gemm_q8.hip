@@ -118,6 +118,8 @@ struct Q8Args {
   int64_t m, n, k;
   int64_t pitch_words;  // pitch / 4
   int64_t a_bytes, b_bytes;
+  int32_t* part;        // split k: [splits][m][n] Int32 partial sums, else nullptr
+  int64_t sps;          // 128-code slices per split (blockIdx.y)
   int tiles_n;
 };
 
@@ -160,16 +162,18 @@ __global__ void __launch_bounds__(NTHREADS) q8_gemm_kernel(Q8Args g) {
   const int64_t i0 = (int64_t)(blockIdx.x / g.tiles_n) * BM;
   const int64_t j0 = (int64_t)(blockIdx.x % g.tiles_n) * BN;
   const int64_t nslices = (g.k + Q8_KS - 1) / Q8_KS;
+  const int64_t kt0 = (int64_t)blockIdx.y * g.sps;
+  const int64_t kt1 = kt0 + g.sps < nslices ? kt0 + g.sps : nslices;
 
   DirectLoader<T_F32, true> lda, ldb;
   lda.init(g.pitch_words, wave, lane);
   ldb.init(g.pitch_words, wave, lane);
   constexpr int LPS = 2 * Slice<T_F32, true>::PER_WAVE;
   constexpr int WAIT_ONE_BEHIND = (LPS & 0xF) | ((LPS >> 4) << 14) | (0x7 << 4) | (0xF << 8);
-  lda.issue(lds0[0], g.qa, g.a_bytes, g.pitch_words, i0, 0, wave);
-  ldb.issue(lds0[1], g.qb, g.b_bytes, g.pitch_words, j0, 0, wave);
-  lda.issue(lds1[0], g.qa, g.a_bytes, g.pitch_words, i0, KT, wave);
-  ldb.issue(lds1[1], g.qb, g.b_bytes, g.pitch_words, j0, KT, wave);
+  lda.issue(lds0[0], g.qa, g.a_bytes, g.pitch_words, i0, kt0 * KT, wave);
+  ldb.issue(lds0[1], g.qb, g.b_bytes, g.pitch_words, j0, kt0 * KT, wave);
+  lda.issue(lds1[0], g.qa, g.a_bytes, g.pitch_words, i0, (kt0 + 1) * KT, wave);
+  ldb.issue(lds1[1], g.qb, g.b_bytes, g.pitch_words, j0, (kt0 + 1) * KT, wave);
 
   const int bcol = wc * 32 + (lane & 31);
   v16i acc[2];
@@ -193,11 +197,11 @@ __global__ void __launch_bounds__(NTHREADS) q8_gemm_kernel(Q8Args g) {
     __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND);                                                 \
     lds_barrier();                                                                               \
   } while (0)
-  for (int64_t kt = 0; kt < nslices;) {
+  for (int64_t kt = kt0; kt < kt1;) {
     MLG_Q8_STEP(lds0, lds2);
-    if (++kt >= nslices) break;
+    if (++kt >= kt1) break;
     MLG_Q8_STEP(lds1, lds0);
-    if (++kt >= nslices) break;
+    if (++kt >= kt1) break;
     MLG_Q8_STEP(lds2, lds1);
     ++kt;
   }
@@ -206,6 +210,18 @@ __global__ void __launch_bounds__(NTHREADS) q8_gemm_kernel(Q8Args g) {
 
   const int64_t col = j0 + bcol;
   if (col >= g.n) return;
+  if (g.part != nullptr) {  // split k: the exact partial sums, folded by q8_reduce_kernel
+    int32_t* pr = g.part + (int64_t)blockIdx.y * g.m * g.n;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = i0 + wr * 64 + 32 * blk + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+        if (row < g.m) pr[row * g.n + col] = acc[blk][r];
+      }
+    }
+    return;
+  }
   const int64_t eb = g.eb[col];
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
@@ -215,6 +231,17 @@ __global__ void __launch_bounds__(NTHREADS) q8_gemm_kernel(Q8Args g) {
       if (row < g.m) g.c[row * g.n + col] = q8_dequant(acc[blk][r], (int64_t)g.ea[row] + eb);
     }
   }
+}
+
+// The split-k fold: Int32 addition is exact and associative (every partial and every running
+// sum is bounded by 16129 * k < 2^31), so adding the splits in order gives the one-pass sum.
+__global__ void q8_reduce_kernel(float* c, const int32_t* part, const int32_t* ea, const int32_t* eb, int64_t m,
+                                 int64_t n, int splits) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= m * n) return;
+  int32_t acc = 0;
+  for (int s = 0; s < splits; ++s) acc += part[s * m * n + i];
+  c[i] = q8_dequant(acc, (int64_t)ea[i / n] + eb[i % n]);
 }
 
 __global__ void q8_repack_kernel(int8_t* dst, const int8_t* src, int64_t rows, int64_t k, int64_t pitch) {
@@ -230,10 +257,28 @@ __global__ void q8_repack_kernel(int8_t* dst, const int8_t* src, int64_t rows, i
 static bool q8_in_place(const void* p, int64_t k) { return k % 16 == 0 && ((uintptr_t)p % 16u) == 0; }
 static int64_t q8_pitch(int64_t k) { return (k + 15) / 16 * 16; }
 
-int64_t q8_workspace_bytes(const void* qa, const void* qb, int64_t m, int64_t n, int64_t k) {
+// Split k when the output tiles leave CUs idle (the skinny decode rows): about two workgroups
+// per CU, at least two slices per split, the partial sums capped at 64 MB.
+static int64_t q8_splits(int64_t m, int64_t n, int64_t k, int num_cus, int64_t* sps) {
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  const int64_t nslices = (k + Q8_KS - 1) / Q8_KS;
+  int64_t want = tiles >= num_cus ? 1 : (2 * (int64_t)num_cus + tiles - 1) / tiles;
+  if (want > nslices / 2) want = nslices / 2;
+  while (want > 1 && want * m * n * 4 > (int64_t(64) << 20)) --want;
+  if (want < 1) want = 1;
+  *sps = (nslices + want - 1) / want;
+  return (nslices + *sps - 1) / *sps;
+}
+
+static int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
+
+int64_t q8_workspace_bytes(const void* qa, const void* qb, int64_t m, int64_t n, int64_t k, int num_cus) {
   int64_t bytes = 0;
-  if (!q8_in_place(qa, k)) bytes += (m * q8_pitch(k) + 255) / 256 * 256;
-  if (!q8_in_place(qb, k)) bytes += (n * q8_pitch(k) + 255) / 256 * 256;
+  if (!q8_in_place(qa, k)) bytes += round256(m * q8_pitch(k));
+  if (!q8_in_place(qb, k)) bytes += round256(n * q8_pitch(k));
+  int64_t sps;
+  const int64_t splits = q8_splits(m, n, k, num_cus, &sps);
+  if (splits > 1) bytes += round256(splits * m * n * 4);
   return bytes;
 }
 
@@ -255,7 +300,6 @@ hipError_t run_q8_dequantize(float* out, const int8_t* codes, const int32_t* exp
 
 hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
                        int64_t m, int64_t n, int64_t k, void* ws, int num_cus, hipStream_t stream) {
-  (void)num_cus;
   if (m <= 0 || n <= 0 || k <= 0 || k > INT8_MAX_K) return hipErrorInvalidValue;
   const int64_t pitch = q8_pitch(k);
   if (32 * pitch + Q8_KS >= (int64_t(1) << 31)) return hipErrorInvalidValue;
@@ -271,7 +315,14 @@ hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     ops[w] = wsp;
-    wsp += (total + 255) / 256 * 256;
+    wsp += round256(total);
+  }
+  int64_t sps;
+  const int64_t splits = q8_splits(m, n, k, num_cus, &sps);
+  int32_t* part = nullptr;
+  if (splits > 1) {
+    if (wsp == nullptr) return hipErrorInvalidValue;
+    part = reinterpret_cast<int32_t*>(wsp);
   }
   Q8Args g;
   g.c = c; g.qa = ops[0]; g.qb = ops[1]; g.ea = ea; g.eb = eb;
@@ -281,7 +332,13 @@ hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8
   g.b_bytes = n * pitch;
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   g.tiles_n = (int)tn;
-  hipLaunchKernelGGL(q8_gemm_kernel, dim3((unsigned)(tm * tn)), dim3(NTHREADS), 0, stream, g);
+  g.part = part;
+  g.sps = sps;
+  hipLaunchKernelGGL(q8_gemm_kernel, dim3((unsigned)(tm * tn), (unsigned)splits), dim3(NTHREADS), 0, stream, g);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  hipLaunchKernelGGL(q8_reduce_kernel, dim3((unsigned)((m * n + 255) / 256)), dim3(256), 0, stream, c, part, ea, eb,
+                     m, n, (int)splits);
   return hipGetLastError();
 }
 

@@ -16,9 +16,10 @@ hipError_t run_q8_quantize(int8_t* codes, int32_t* exps, const float* x, int64_t
 hipError_t run_q8_dequantize(float* out, const int8_t* codes, const int32_t* exps, int64_t rows, int64_t cols,
                              hipStream_t stream);
 
-// Workspace bytes run_q8_gemm needs (operand rows not a multiple of 16 bytes, or a base not
-// 16-byte aligned, are repacked with zero codes).
-int64_t q8_workspace_bytes(const void* qa, const void* qb, int64_t m, int64_t n, int64_t k);
+// Workspace bytes run_q8_gemm needs on a device of `num_cus` CUs: operand rows not a multiple
+// of 16 bytes, or a base not 16-byte aligned, are repacked with zero codes; a product whose
+// output tiles leave CUs idle splits k and keeps Int32 partial sums.
+int64_t q8_workspace_bytes(const void* qa, const void* qb, int64_t m, int64_t n, int64_t k, int num_cus);
 
 // C = qa . qb^T (OP_NT): C[i][j] = ftz(f32(sum_p qa[i][p] qb[j][p]) * 2^(ea[i] + eb[j])), the sum
 // exact in Int32 (k <= INT8_MAX_K), f32 by the pinned split conversion; NaN words canonical.

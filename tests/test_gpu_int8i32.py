@@ -33,8 +33,10 @@ def _bits_equal(got, want, what):
                            f"got {g[bad[0]]:#010x} want {w[bad[0]]:#010x}")
 
 
+# (1, 4096, 4096), (8, 300, 14336), (3, 1000, 1000), (33, 47, 131072) and (16, 129, 385) split k.
 SHAPES = [(1, 1, 1), (3, 5, 7), (1, 300, 16), (130, 129, 16), (128, 128, 128), (129, 257, 129),
-          (200, 300, 4097), (64, 1000, 520), (300, 64, 2048), (33, 47, 131072), (512, 512, 512)]
+          (200, 300, 4097), (64, 1000, 520), (300, 64, 2048), (33, 47, 131072), (512, 512, 512),
+          (1, 4096, 4096), (8, 300, 14336), (3, 1000, 1000), (16, 129, 385)]
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in SHAPES])
@@ -151,3 +153,43 @@ def test_surface_matmul_int8_forms(oracle):
         linalg.matmul_int8(a, b[:, :999])
     with pytest.raises(ValueError, match=r"a exponents has shape \(44,\), want \(45,\)"):
         linalg.matmul_int8((qa, ea[:44]), b)
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 4096), (200, 300, 4097), (8, 300, 1000)])
+def test_gemm_int8i32_ws_in_graph(oracle, shape):
+    """The caller-workspace entry (split-k partials, repack) captured in a HIP graph and
+    replayed three times, eager work between replays; every replay bit-identical."""
+    from mojolearn_amd import _native
+    m, n, k = shape
+    rng = np.random.default_rng(k)
+    qa = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qb = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    ea = rng.integers(-30, 30, m).astype(np.int32)
+    eb = rng.integers(-30, 30, n).astype(np.int32)
+    want = oracle.nan_canon(oracle.q8_gemm(qa, ea, qb, eb))
+    L = _native.lib()
+    ta, tb, tea, teb = _t(qa), _t(qb), _t(ea), _t(eb)
+    nb = L.mlg_gemm_int8i32_workspace_bytes(ta.data_ptr(), tb.data_ptr(), m, n, k)
+    assert nb >= 0
+    ws = torch.empty(max(nb, 4), dtype=torch.uint8, device=DEV)
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    s = torch.cuda.Stream()
+
+    def call():
+        _native.check(L.mlg_gemm_int8i32_ws(out.data_ptr(), ta.data_ptr(), tea.data_ptr(), tb.data_ptr(),
+                                            teb.data_ptr(), m, n, k, ws.data_ptr(), nb, s.cuda_stream))
+
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.synchronize()
+    _bits_equal(out.cpu().numpy(), want, "eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        call()
+    for r in range(3):
+        out.fill_(-1.0)
+        ws.fill_(0x5A)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _bits_equal(out.cpu().numpy(), want, f"replay {r}")
