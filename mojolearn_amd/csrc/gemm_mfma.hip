@@ -199,15 +199,49 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND); \
     lds_barrier(); \
   } while (0)
+  // The regular case (every decoder shape: leaves of whole slices, k a multiple of KT):
+  // every slice runs all KT steps, and a leaf ends after exactly `spl` slices.
+#define MLG_REGULAR_STEP(CUR, FILL) \
+  do { \
+    lda.issue(FILL[0], g.a, g.a_bytes, g.a_pitch, i0, (kt + 2) * KT, wave); \
+    ldb.issue(FILL[1], g.b, g.b_bytes, g.b_pitch, j0, (kt + 2) * KT, wave); \
+    mfma_steps<OP, AT, BT, true>(acc, CUR[0], CUR[1], 0, KT, arow, bcol, scale); \
+    if (++sl == spl) { \
+      sl = 0; \
+      if (t + 1 < cnt) { \
+        stk.push(acc, t); \
+        _Pragma("unroll") for (int e = 0; e < 32; ++e) acc[e] = 0.f; \
+        ++t; \
+      } else { \
+        acc = stk.root(acc, t); \
+      } \
+    } \
+    __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND); \
+    lds_barrier(); \
+  } while (0)
   static_assert(NBUF == 3, "the slice loop is unrolled by NBUF");
-  for (int64_t kt = kt_first; kt <= kt_last;) {
-    MLG_SLICE_STEP(lds0, lds2);
-    if (++kt > kt_last) break;
-    MLG_SLICE_STEP(lds1, lds0);
-    if (++kt > kt_last) break;
-    MLG_SLICE_STEP(lds2, lds1);
-    ++kt;
+  if (g.leaf % KT == 0 && ke % KT == 0) {
+    const int spl = (int)(g.leaf / KT);
+    int sl = 0;
+    for (int64_t kt = kt_first; kt <= kt_last;) {
+      MLG_REGULAR_STEP(lds0, lds2);
+      if (++kt > kt_last) break;
+      MLG_REGULAR_STEP(lds1, lds0);
+      if (++kt > kt_last) break;
+      MLG_REGULAR_STEP(lds2, lds1);
+      ++kt;
+    }
+  } else {
+    for (int64_t kt = kt_first; kt <= kt_last;) {
+      MLG_SLICE_STEP(lds0, lds2);
+      if (++kt > kt_last) break;
+      MLG_SLICE_STEP(lds1, lds0);
+      if (++kt > kt_last) break;
+      MLG_SLICE_STEP(lds2, lds1);
+      ++kt;
+    }
   }
+#undef MLG_REGULAR_STEP
 #undef MLG_SLICE_STEP
   // no load into LDS may outlive the workgroup
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)

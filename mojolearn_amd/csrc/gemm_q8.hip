@@ -302,7 +302,7 @@ hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8
                        int64_t m, int64_t n, int64_t k, void* ws, int num_cus, hipStream_t stream) {
   if (m <= 0 || n <= 0 || k <= 0 || k > INT8_MAX_K) return hipErrorInvalidValue;
   const int64_t pitch = q8_pitch(k);
-  if (32 * pitch + Q8_KS >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  if (32 * pitch + Q8_KS >= (int64_t(1) << 30)) return hipErrorInvalidValue;
   char* wsp = static_cast<char*>(ws);
   const void* ops[2] = {qa, qb};
   const int64_t rows[2] = {m, n};

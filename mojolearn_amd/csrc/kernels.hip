@@ -137,8 +137,10 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
     }
     if (is_a) { g.a = src; g.a_pitch = pitch; g.a_bytes = rows * pitch * eb; }
     else { g.b = src; g.b_pitch = pitch; g.b_bytes = rows * pitch * eb; }
-    // one load instruction spans at most 32 stored rows (int8, index-major)
-    if ((32 * pitch + KT) * eb >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+    // one load instruction spans at most 32 stored rows (int8, index-major), and a slice
+    // advances a k-major operand by KT rows: both below 2^30 bytes keep the loads' lane and
+    // scalar offsets below 2^31
+    if ((32 * pitch + KT) * eb >= (int64_t(1) << 30)) return hipErrorInvalidValue;
   }
   dim3 grid((unsigned)(tm * tn), (unsigned)g.ngroups);
   hipError_t e = launch_mfma(g, p.op, p.a_type, p.b_type, grid, stream);

@@ -41,17 +41,24 @@ struct Slice {
 
 // The global side of one operand: this lane's share of every slice's load instructions, as
 // buffer loads straight into LDS.  Load instruction q of a slice covers RPI consecutive
-// stored rows; its scalar resource starts at the first of them and ends at the operand's
-// end, and the lane's byte offset within it is fixed for the whole k loop.  A chunk past
-// the operand's end reads as zeros (the resource's record bound); a chunk past a row's
-// end reads the next row's bytes.  Neither reaches a stored cell: indices past m or n are
-// never stored, steps past k are never executed.  The host keeps RPI * pitch * bytes
-// below 2^31.
+// stored rows; its scalar resource starts at the first of them (at the step where the
+// resource was built) and ends at the operand's end, and the lane's byte offset within it
+// is fixed for the whole k loop.  Slices are issued in ascending order, one slice apart, so
+// a slice's loads differ from the previous slice's only by a scalar offset (SOFF_STEP bytes
+// per step); the resources are rebuilt only when that offset passes 2^30 (never for an
+// index-major operand of fewer than 2^28 steps).  A chunk past the operand's end reads as
+// zeros (the resource's record bound, exact because lane offset + scalar offset stays below
+// 2^31); a chunk past a row's end reads the next row's bytes.  Neither reaches a stored
+// cell: indices past m or n are never stored, steps past k are never executed.  The host
+// keeps RPI * pitch * bytes below 2^30.
 template <int T, bool IMAJ>
 struct DirectLoader {
   using S = Slice<T, IMAJ>;
   static constexpr int RPI = IMAJ ? 64 / S::CR : 64 / S::RC;  // stored rows per instruction
   uint32_t voff[S::PER_WAVE];
+  __amdgpu_buffer_rsrc_t rs[S::PER_WAVE];
+  uint32_t soff;        // bytes from the resources' step to the next slice's first step
+  uint32_t slice_step;  // bytes one slice advances the scalar offset
 
   __device__ __forceinline__ void init(int64_t pitch, int wave, int lane) {
 #pragma unroll
@@ -62,14 +69,13 @@ struct DirectLoader {
       if constexpr (IMAJ) voff[h] = (uint32_t)(((di - q * RPI) * pitch + dk) * S::EB);
       else voff[h] = (uint32_t)(((dk - q * RPI) * pitch + di) * S::EB);
     }
+    slice_step = (uint32_t)(IMAJ ? KT * S::EB : KT * pitch * S::EB);
+    soff = 0x7FFFFFFFu;  // the first issue builds the resources
   }
 
-  // Issue this wave's PER_WAVE loads of the slice that starts at step k0 into `slice` (when
-  // a slice has fewer load instructions than waves, the extra waves repeat an earlier
-  // wave's chunk -- the same bytes to the same place -- so every wave issues the same
-  // count and can wait on it with one vmcnt).  `wave` must be wave-uniform.
-  __device__ __forceinline__ void issue(char* slice, const void* base, int64_t total_bytes, int64_t pitch,
-                                        int64_t idx0, int64_t k0, int wave) const {
+  // Resources for the slice that starts at step k0; the scalar offset restarts at 0.
+  __device__ __forceinline__ void bind(const void* base, int64_t total_bytes, int64_t pitch, int64_t idx0,
+                                       int64_t k0, int wave) {
 #pragma unroll
     for (int h = 0; h < S::PER_WAVE; ++h) {
       const int q = (wave + NWAVES * h) % S::NI;
@@ -77,16 +83,31 @@ struct DirectLoader {
       const int64_t rem = total_bytes - off;
       const int nrec = rem <= 0 ? 0 : (rem > 0x7FFFFFFF ? 0x7FFFFFFF : (int)rem);
       const char* first = static_cast<const char*>(base) + (rem > 0 ? off : 0);
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(first), (short)0, nrec, RSRC_WORD3);
+      rs[h] = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(first), (short)0, nrec, RSRC_WORD3);
+    }
+    soff = 0;
+  }
+
+  // Issue this wave's PER_WAVE loads of the slice that starts at step k0 into `slice`: the
+  // slice after the previously issued one, or the first (when a slice has fewer load
+  // instructions than waves, the extra waves repeat an earlier wave's chunk -- the same
+  // bytes to the same place -- so every wave issues the same count and can wait on it with
+  // one vmcnt).  `wave` must be wave-uniform.
+  __device__ __forceinline__ void issue(char* slice, const void* base, int64_t total_bytes, int64_t pitch,
+                                        int64_t idx0, int64_t k0, int wave) {
+    if (soff > (1u << 30)) bind(base, total_bytes, pitch, idx0, k0, wave);
+#pragma unroll
+    for (int h = 0; h < S::PER_WAVE; ++h) {
+      const int q = (wave + NWAVES * h) % S::NI;
 #if defined(__HIP_DEVICE_COMPILE__)
       // (the host pass compiles kernel bodies only for their launch stubs; with this builtin
       // in a kernel template it drops the stubs of every instantiation after the first)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_vptr)(slice + q * 1024), 16, voff[h], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs[h], (lds_vptr)(slice + q * 1024), 16, voff[h], soff, 0, 0);
 #else
-      (void)rs;
+      (void)slice;
 #endif
     }
+    soff += slice_step;
   }
 };
 
