@@ -66,7 +66,7 @@ struct Stack32 {
 // a step outside [s0, s1) is skipped by a uniform branch.  The scheduling fences keep the
 // compiler from hoisting every LDS read of the slice, which would not fit beside the
 // accumulator and the fold slots.
-template <int OP, int AT, int BT, bool FULL>
+template <int OP, int AT, int BT, bool FULL, bool FRESH = false>
 __device__ __forceinline__ void mfma_steps(v32f& acc, const char* la, const char* lb, int s0, int s1,
                                            int arow, int bcol, float scale) {
   constexpr bool A_IMAJ = (OP != OP_TN);
@@ -82,8 +82,11 @@ __device__ __forceinline__ void mfma_steps(v32f& acc, const char* la, const char
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (FULL || (s + q >= s0 && s + q < s1)) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[q], b4[q], acc, 0, 0, 0);
+    for (int q = 0; q < 4; ++q) {
+      // FRESH: the slice starts a leaf, whose chain starts from +0 (the MFMA's C operand)
+      if (FRESH && s + q == 0) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[q], b4[q], v32f{}, 0, 0, 0);
+      else if (FULL || (s + q >= s0 && s + q < s1)) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a4[q], b4[q], acc, 0, 0, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (s + 4 < KT) { a4 = an; b4 = bn; }
   }
@@ -205,12 +208,12 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   do { \
     lda.issue(FILL[0], g.a, g.a_bytes, g.a_pitch, i0, (kt + 2) * KT, wave); \
     ldb.issue(FILL[1], g.b, g.b_bytes, g.b_pitch, j0, (kt + 2) * KT, wave); \
-    mfma_steps<OP, AT, BT, true>(acc, CUR[0], CUR[1], 0, KT, arow, bcol, scale); \
+    if (sl == 0) mfma_steps<OP, AT, BT, true, true>(acc, CUR[0], CUR[1], 0, KT, arow, bcol, scale); \
+    else mfma_steps<OP, AT, BT, true>(acc, CUR[0], CUR[1], 0, KT, arow, bcol, scale); \
     if (++sl == spl) { \
       sl = 0; \
       if (t + 1 < cnt) { \
         stk.push(acc, t); \
-        _Pragma("unroll") for (int e = 0; e < 32; ++e) acc[e] = 0.f; \
         ++t; \
       } else { \
         acc = stk.root(acc, t); \
