@@ -23,7 +23,7 @@ constexpr int GV_THREADS = 256;
 constexpr int GV_LEAVES = GV_THREADS / 64;  // leaves per workgroup: an aligned subtree
 constexpr int GV_MAXM = 16;
 constexpr int GV_CH = 128;                  // W rows per register buffer: a whole contract leaf
-constexpr int GV_FOLD_BATCH = 32;           // root loads in flight while folding
+constexpr int GV_FOLD_BATCH = 16;           // root loads in flight while folding
 constexpr int GV_FEW_GROUPS = 8;            // up to this many groups: all roots loaded at once
 
 template <int T, bool NT = false>
@@ -44,9 +44,14 @@ struct GemvArgs {
   int64_t ncg;            // column groups
 };
 
+// OP_NN with whole 128-row leaves and at least this many rows of X: the chains on the matrix
+// cores (gemv_mfma.hip; X 16-byte aligned, 16 * K * 4 < 2^31).
+constexpr int GV_MFMA_MIN_M = 5;
+
 // vec (OP_NN): 0 element loads, 1 word (buffer) loads, 2 word loads of whole 128-row leaves.
 hipError_t launch_gemv_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,
                           hipStream_t stream);
+hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, dim3 grid, hipStream_t stream);
 // vec (OP_NT): 0 element loads, 1 16-byte loads.
 hipError_t launch_gemv_nt(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,
                           hipStream_t stream);

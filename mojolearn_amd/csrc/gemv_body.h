@@ -290,6 +290,114 @@ __device__ __forceinline__ void gv_leaf_nt(float (&acc)[MR][1], const char* w, i
   }
 }
 
+// The end of a skinny product, once every wave has written its leaf partial into
+// part[wave][row][col]: the workgroup's root (the tree over its up to GV_LEAVES leaves),
+// then either the store (one group) or the count and, in the workgroup that completes it,
+// the fold of every group's root (the rest of the contract's tree), bias and store.
+template <int MR, int COLS>
+__device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[GV_LEAVES][MR][COLS],
+                                          unsigned int& last_flag, int tid, int64_t grp, int64_t cg, int m) {
+  __syncthreads();
+  const int64_t left = g.nleaves - grp * GV_LEAVES;
+  const int cnt = left < GV_LEAVES ? (int)left : GV_LEAVES;
+  constexpr int CPT = (MR * COLS + GV_THREADS - 1) / GV_THREADS;  // cells per thread
+  constexpr int LB = CPT < 4 ? CPT : 4;                            // cells per batch of LDS reads
+  // this thread's cells tid + c * GV_THREADS of rows < m, LB at a time: every partial of a
+  // batch read before any add
+#pragma unroll
+  for (int c0 = 0; c0 < CPT; c0 += LB) {
+    float p[GV_LEAVES][LB];
+#pragma unroll
+    for (int c = 0; c < LB; ++c) {
+      const int cell = tid + (c0 + c) * GV_THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      if (c0 + c >= CPT || cell >= MR * COLS || r >= m) continue;
+#pragma unroll
+      for (int l = 0; l < GV_LEAVES; ++l)
+        if (l < cnt) p[l][c] = part[l][r][col];
+    }
+#pragma unroll
+    for (int c = 0; c < LB; ++c) {
+      const int cell = tid + (c0 + c) * GV_THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
+      float y = p[0][c];
+      if (cnt >= 2) y = y + p[1][c];           // leaves 0,1 paired
+      if (cnt == 3) y = y + p[2][c];           // leaf 2 carried, then joined
+      if (cnt == 4) y = y + (p[2][c] + p[3][c]);
+      if (g.ngroups == 1) {
+        if (g.bias) y = y + g.bias[j];  // ftz(C) + ftz(b) by the input flush
+        g.c[r * g.n + j] = store_word(y);
+      } else {
+        __hip_atomic_store(&g.ws[(grp * g.m + r) * g.n + j], y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (g.ngroups == 1) return;
+
+  // Count this group's roots in; the workgroup that completes the count folds.  The roots
+  // are device-coherent stores, complete (vmcnt) before the count is published.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int prev = __hip_atomic_fetch_add(&g.counter[cg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = prev + 1 == (unsigned int)g.ngroups ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  const int64_t stride = g.m * g.n;
+  if (g.ngroups <= GV_FEW_GROUPS) {
+    // every root of up to 8 cells of this thread requested at once, then folded
+    constexpr int CB = CPT < 8 ? CPT : 8;
+#pragma unroll
+    for (int c0 = 0; c0 < CPT; c0 += CB) {
+      float v[CB][GV_FEW_GROUPS];
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        const int cell = tid + (c0 + c) * GV_THREADS;
+        const int r = cell / COLS, col = cell % COLS;
+        const int64_t j = cg * COLS + col;
+        if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
+#pragma unroll
+        for (int e = 0; e < GV_FEW_GROUPS; ++e)
+          if (e < g.ngroups)
+            v[c][e] = __hip_atomic_load(g.ws + (e * g.m + r) * g.n + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        const int cell = tid + (c0 + c) * GV_THREADS;
+        const int r = cell / COLS, col = cell % COLS;
+        const int64_t j = cg * COLS + col;
+        if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
+        StackF stk;
+        const int P = (int)g.ngroups;
+#pragma unroll
+        for (int e = 0; e + 1 < GV_FEW_GROUPS; ++e)
+          if (e + 1 < P) stk.push(v[c][e], e);
+        float y = v[c][0];
+#pragma unroll
+        for (int e = 1; e < GV_FEW_GROUPS; ++e)
+          if (e == P - 1) y = v[c][e];
+        y = stk.root(y, P - 1);
+        if (g.bias) y = y + g.bias[j];
+        g.c[r * g.n + j] = store_word(y);
+      }
+    }
+  } else {
+#pragma unroll 1
+    for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (r >= m || j >= g.n) continue;
+      float y = fold_roots(g.ws + r * g.n + j, g.ngroups, stride);
+      if (g.bias) y = y + g.bias[j];
+      g.c[r * g.n + j] = store_word(y);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&g.counter[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One skinny product: OP_NN (W[k][n], FULLLEAF: every leaf exactly 128 rows) or OP_NT (W[n][k]).
 template <int BT, int MR, bool VEC, bool FULLLEAF, bool NT>
 __device__ __forceinline__ void gemv_body(const GemvArgs& g, const float* __restrict__ x) {
@@ -370,82 +478,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, const float* __rest
   for (int r = 0; r < MR; ++r)
 #pragma unroll
     for (int e = 0; e < CPL; ++e) part[wave][r][lane * CPL + e] = acc[r][e];
-  __syncthreads();
-  const int64_t left = g.nleaves - grp * GV_LEAVES;
-  const int cnt = left < GV_LEAVES ? (int)left : GV_LEAVES;
-  for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
-    const int r = cell / COLS, col = cell % COLS;
-    const int64_t j = cg * COLS + col;
-    if (r >= m || j >= g.n) continue;
-    float y = part[0][r][col];
-    if (cnt >= 2) y = y + part[1][r][col];           // leaves 0,1 paired
-    if (cnt == 3) y = y + part[2][r][col];           // leaf 2 carried, then joined
-    if (cnt == 4) y = y + (part[2][r][col] + part[3][r][col]);
-    if (g.ngroups == 1) {
-      if (g.bias) y = y + g.bias[j];  // ftz(C) + ftz(b) by the input flush
-      g.c[r * g.n + j] = store_word(y);
-    } else {
-      __hip_atomic_store(&g.ws[(grp * g.m + r) * g.n + j], y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  if (g.ngroups == 1) return;
-
-  // Count this group's roots in; the workgroup that completes the count folds.  The roots
-  // are device-coherent stores, complete (vmcnt) before the count is published.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned int prev = __hip_atomic_fetch_add(&g.counter[cg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = prev + 1 == (unsigned int)g.ngroups ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  const int64_t stride = g.m * g.n;
-  constexpr int CPT = (MR * COLS + GV_THREADS - 1) / GV_THREADS;  // cells per thread
-  if (g.ngroups <= GV_FEW_GROUPS) {
-    // every root of every cell of this thread requested at once, then folded
-    float v[CPT][GV_FEW_GROUPS];
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int cell = tid + c * GV_THREADS;
-      const int r = cell / COLS, col = cell % COLS;
-      const int64_t j = cg * COLS + col;
-      if (cell >= MR * COLS || r >= m || j >= g.n) continue;
-#pragma unroll
-      for (int e = 0; e < GV_FEW_GROUPS; ++e)
-        if (e < g.ngroups)
-          v[c][e] = __hip_atomic_load(g.ws + (e * g.m + r) * g.n + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int cell = tid + c * GV_THREADS;
-      const int r = cell / COLS, col = cell % COLS;
-      const int64_t j = cg * COLS + col;
-      if (cell >= MR * COLS || r >= m || j >= g.n) continue;
-      StackF stk;
-      const int P = (int)g.ngroups;
-#pragma unroll
-      for (int e = 0; e + 1 < GV_FEW_GROUPS; ++e)
-        if (e + 1 < P) stk.push(v[c][e], e);
-      float y = v[c][0];
-#pragma unroll
-      for (int e = 1; e < GV_FEW_GROUPS; ++e)
-        if (e == P - 1) y = v[c][e];
-      y = stk.root(y, P - 1);
-      if (g.bias) y = y + g.bias[j];
-      g.c[r * g.n + j] = store_word(y);
-    }
-  } else {
-    for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
-      const int r = cell / COLS, col = cell % COLS;
-      const int64_t j = cg * COLS + col;
-      if (r >= m || j >= g.n) continue;
-      float y = fold_roots(g.ws + r * g.n + j, g.ngroups, stride);
-      if (g.bias) y = y + g.bias[j];
-      g.c[r * g.n + j] = store_word(y);
-    }
-  }
-  if (tid == 0) __hip_atomic_store(&g.counter[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  gv_finish<MR, COLS>(g, part, last_flag, tid, grp, cg, m);
 }
 
 }  // namespace mlg

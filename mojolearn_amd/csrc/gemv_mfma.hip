@@ -1,0 +1,152 @@
+// gfx950 skinny-M kernel on the matrix cores, OP_NN with whole 128-row leaves: X[M x K] . W[K x N]
+// for 5 <= M <= 16 (the decode batches whose VALU chains would outweigh the weight stream).
+//
+// Same work split as gemv_nn_kernel: a wave owns one k-leaf of one column group, a lane one
+// 32-bit word of every W row (CPL columns), the rows streamed through a register ring.  The
+// chains run on v_mfma_f32_16x16x1_4b_f32: four 16 x 16 blocks with K = 1, one fma_rn per output
+// element (under MODE.FP_DENORM = 2 it is fma(ftz a, ftz b, ftz c), like v_fma_f32 and the
+// K=1 MFMA of the tile kernel).  For byte e of the lane words, lane l feeds A = x[l % 16][p]
+// and B = W[p][CPL*l + e], so block l / 16 of the instruction computes rows 0..15 of the 16
+// columns {CPL*(16*(l/16) + j) + e : j < 16}; one instruction per word byte per k step
+// advances 16 x 64 chains by one step.  The leaf's first step takes +0 as its C operand.
+// The epilogue (leaf partials through LDS, the group's subtree, the cross-workgroup fold)
+// is gemv_nn_kernel's.
+#include "gemv_body.h"
+
+namespace mlg {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// The wave's x block, rows 0..15 (rows past m repeat row m-1) by the leaf's 128 steps, staged
+// in its own LDS area xs[16][GV_CH] before the W ring is requested: x then comes from LDS
+// (lgkmcnt) and never makes the loop wait behind the ring's loads (vmcnt is in order).
+constexpr int GV_XS = 16 * GV_CH;  // floats of one wave's x block
+constexpr int MF_RB = 16;          // W rows per ring block
+constexpr int MF_AHEAD = 7;        // blocks requested ahead: the whole leaf in flight
+
+template <int BT>
+__device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
+                                             int rowbytes, const float* __restrict__ xl, int64_t k, int m,
+                                             float* xs, int lane, const float (&sc)[GvCols<BT>::cpl]) {
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int NBLK = GV_CH / MF_RB;
+  constexpr int RING = MF_AHEAD + 1;
+  // lane l stages row l / 4, steps 32 * (l % 4) .. +31 (x + kb is 16-byte aligned: the host
+  // requires an aligned x and k a multiple of 128)
+  {
+    const int r = lane >> 2;
+    const f4* src = reinterpret_cast<const f4*>(xl + (int64_t)(r < m ? r : m - 1) * k + 32 * (lane & 3));
+    f4 v[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = src[c];
+    f4* dst = reinterpret_cast<f4*>(xs + r * GV_CH + 32 * (lane & 3));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) dst[c] = v[c];
+  }
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
+
+  uint32_t ring[RING][MF_RB];
+#pragma unroll
+  for (int b = 0; b < MF_AHEAD; ++b)
+#pragma unroll
+    for (int i = 0; i < MF_RB; ++i)
+      ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * MF_RB + i) * rowbytes, 0);
+  // x[row][p .. p+3] for this lane's row (l % 16), four steps per LDS read
+  const f4* xrow = reinterpret_cast<const f4*>(xs + (lane & 15) * GV_CH);
+  f4 xc = xrow[0], xn;
+
+#pragma unroll
+  for (int b = 0; b < NBLK; ++b) {
+    if (b + MF_AHEAD < NBLK) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < MF_RB; ++i)
+        ring[(b + MF_AHEAD) % RING][i] =
+            __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ((b + MF_AHEAD) * MF_RB + i) * rowbytes, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q0 = 0; q0 < MF_RB; q0 += 4) {
+      const int s0 = b * MF_RB + q0;
+      if (s0 + 4 < GV_CH) xn = xrow[(s0 + 4) / 4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float wv[CPL];
+        gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
+        const float xa = xc[q];
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+          if (s0 + q == 0) acc[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(xa, wv[e], v16f{}, 0, 0, 0);
+          else acc[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(xa, wv[e], acc[e], 0, 0, 0);
+        }
+      }
+      if (s0 + 4 < GV_CH) xc = xn;
+    }
+  }
+}
+
+template <int BT>
+__global__ void __launch_bounds__(GV_THREADS) gemv_mfma_nn_kernel(GemvArgs g, const float* __restrict__ x) {
+  constexpr int MR = GV_MAXM;
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int COLS = GvCols<BT>::cols;
+  constexpr int EB = Elem<BT>::bytes;
+  // The waves' leaf partials; a wave's x block lives in its own partial area while it runs
+  // its leaf when that area is large enough (int8, bf16), else in an area of its own (f32).
+  constexpr int PART = MR * COLS;
+  constexpr int XOWN = PART >= GV_XS ? 0 : GV_XS;
+  __shared__ __attribute__((aligned(16))) float part[GV_LEAVES][MR][COLS];
+  __shared__ __attribute__((aligned(16))) float xown[GV_LEAVES][XOWN > 0 ? XOWN : 1];
+  __shared__ unsigned int last_flag;
+
+  set_flush_inputs_mode();
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t cg = blockIdx.x % g.ncg;
+  const int64_t grp = blockIdx.x / g.ncg;
+  const int64_t t = grp * GV_LEAVES + wave;  // this wave's leaf
+  const int m = (int)g.m;
+
+  v16f acc[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) acc[e] = v16f{};
+
+  if (t < g.nleaves) {
+    // this lane's columns, clamped into the operand (their cells are never stored)
+    int64_t c0 = cg * COLS + lane * CPL;
+    if (c0 >= g.n) c0 = g.n - CPL;
+    float sc[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      sc[e] = 1.f;
+      if constexpr (BT == T_I8) sc[e] = g.scales[c0 + e];
+    }
+    const int64_t rowbytes = g.n * EB;
+    const int64_t kb = t * GV_CH;
+    gv_leaf_mfma<BT>(acc, static_cast<const char*>(g.w) + kb * rowbytes, (uint32_t)(c0 * EB), (int)rowbytes,
+                     x + kb, g.k, m, XOWN > 0 ? &xown[wave][0] : &part[wave][0][0], lane, sc);
+  }
+
+  // Lane l holds, for word byte e and block blk, rows 4*(l/16)+i of column
+  // CPL*(16*blk + l%16) + e in acc[e][4*blk + i].
+#pragma unroll
+  for (int e = 0; e < CPL; ++e)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        part[wave][4 * (lane >> 4) + i][CPL * (16 * blk + (lane & 15)) + e] = acc[e][4 * blk + i];
+  gv_finish<MR, COLS>(g, part, last_flag, tid, grp, cg, m);
+}
+
+hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, dim3 grid, hipStream_t stream) {
+  if (b_type == T_F32) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_F32>, grid, dim3(GV_THREADS), 0, stream, g, x);
+  else if (b_type == T_BF16) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_BF16>, grid, dim3(GV_THREADS), 0, stream, g, x);
+  else hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_I8>, grid, dim3(GV_THREADS), 0, stream, g, x);
+  return hipGetLastError();
+}
+
+}  // namespace mlg

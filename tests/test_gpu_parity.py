@@ -241,6 +241,41 @@ def test_skinny_m(oracle, shape, wt):
 
 GEMV_NT_SHAPES = GEMV_SHAPES + [(1, 64, 128), (4, 65, 256), (1, 130, 200)]
 
+# 5 <= m <= 16 with whole 128-row leaves: the matrix-core skinny kernel
+GEMV_MFMA_SHAPES = [(5, 257, 1024), (8, 300, 4096), (12, 64, 512), (16, 1024, 128), (16, 4100, 1024),
+                    (9, 1000, 3968), (16, 14336, 4096)]
+
+
+@pytest.mark.parametrize("kind", ["wide", "special"])
+@pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
+@pytest.mark.parametrize("shape", GEMV_MFMA_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_MFMA_SHAPES])
+def test_skinny_m_mfma(oracle, shape, wt, kind):
+    """5 <= m <= 16, whole leaves: the chains on v_mfma_f32_16x16x1_4b_f32 (one fma per step per
+    cell, input flush by the mode), ragged column groups, one to many leaf groups, subnormal,
+    signed-zero, inf and NaN operands, and the fused bias."""
+    D = _dev()
+    m, n, k = shape
+    rng = np.random.default_rng(m * 3 + n + k)
+    x = _values(rng, (m, k), kind)
+    bias = _values(rng, (n,), "wide")
+    print(f"skinny mfma {wt} {kind} m={m} n={n} k={k}", flush=True)
+    tx, tbias = torch.from_numpy(x).to(DEV), torch.from_numpy(bias).to(DEV)
+    if wt == "f32":
+        w = _values(rng, (k, n), kind)
+        got = D.gemm(tx, torch.from_numpy(w).to(DEV), bias=tbias)
+        want = oracle.gemm_fast(x, w, 0)
+    elif wt == "bf16":
+        wb = oracle.bf16_narrow(_values(rng, (k, n), kind))
+        got = D.gemm_bf16w(tx, torch.from_numpy(wb.view(np.int16)).to(DEV), bias=tbias)
+        want = oracle.gemm_fast(x, oracle.bf16_widen(wb), 0)
+    else:
+        codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        got = D.gemm_int8w(tx, torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV), bias=tbias)
+        want = oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0)
+    torch.cuda.synchronize()
+    assert_bits(got.cpu().numpy(), oracle.nan_canon(oracle.bias(want, bias)), f"skinny mfma {wt} {shape}")
+
 
 @pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
 @pytest.mark.parametrize("shape", GEMV_NT_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_NT_SHAPES])
