@@ -18,6 +18,7 @@
  *   - bias add                  transformer/impl/llama/modeling_llama.mojo:3979-3989
  *   - card fill + FNV-1a64      bench/gemm_card_main.mojo:292-311, core/identity_trace.mojo:89-115
  *   - int8i32.v1 (L-3..L-7)     checks/numerics.mojo:1577-1677, gemm/host/gemm_lowbit_oracle.mojo:171-251
+ *   - int15i64.v1 (W-1..W-7)    checks/numerics_int15.mojo:54-175, gemm/host/gemm_int15_oracle.mojo:116-270
  * and a fast threaded arm that computes the same bits (the role of the reference's
  * gemm/host/gemm_host_rows.mojo:467-556): operands flushed once, columns vectorised
  * with AVX2 FMA (one independent chain per column, so no reassociation inside a leaf),
@@ -415,6 +416,109 @@ void orc_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb
       int32_t acc = 0;
       for (int64_t p = 0; p < k; ++p) acc += (int32_t)qa[i * k + p] * (int32_t)qb[j * k + p];
       c[i * n + j] = q8_dequant(acc, (int64_t)ea[i] + (int64_t)eb[j]);
+    }
+}
+
+/* ---- profile mojolearn.identical.gemm.int15i64.v1 (gemm/IDENTICAL_LOWBIT_CONTRACT.md section 6,
+ * W-1..W-7): fifteen-bit codes kept as two int8 planes, hi = floor(c / 128) and lo = c mod 128, an
+ * exact Int64 sum, one pinned conversion, one power-of-two scale; OP_NT only, k <= 65536. */
+
+/* checks/numerics_int15.mojo:54-63 int15_row_exponent (W-1): floor(log2 absmax) - 13. */
+int orc_q15_row_exponent(float absmax) {
+  const float a = ftz(absmax);
+  if (a == 0.0f || a != a) return 0;
+  return (int)((f2u(a) >> 23) & 0xFFu) - 127 - 13;
+}
+
+/* checks/numerics_int15.mojo:66-93 quantize_int15_value (W-2): a NaN codes to 0 before the
+ * scaling and after it (a zero times an infinite 2^-e). */
+static inline int16_t q15_value(float x, int e) {
+  if (x != x) return 0;
+  const float s = ftz(ftz(x) * pow2_f32(-(int64_t)e));
+  if (s != s) return 0;
+  float r = round_half_even_f32(s);
+  if (r > 16383.0f) r = 16383.0f;
+  if (r < -16383.0f) r = -16383.0f;
+  return (int16_t)(int)r;
+}
+
+/* checks/numerics_int15.mojo:96-109 (W-3): the low seven bits, and the arithmetic shift. */
+static inline int8_t q15_lo(int16_t c) { return (int8_t)((int32_t)c & 127); }
+static inline int8_t q15_hi(int16_t c) { return (int8_t)((int32_t)c >> 7); }
+
+/* checks/numerics_int15.mojo:123-163 i64_to_f32_pinned (W-6): below 2^48 two exact 24-bit
+ * conversions, the high one scaled by 2^24, one IEEE addition; from 2^48 the low sixteen bits
+ * fold into a sticky bit and the result is scaled by 2^16. */
+float orc_q15_i64_to_f32(int64_t v) {
+  const int neg = v < 0;
+  uint64_t mag = (uint64_t)v;
+  if (neg) mag = (uint64_t)0 - mag;
+  int reduced = 0;
+  if (mag >= ((uint64_t)1 << 48)) {
+    const uint64_t lost = mag & 0xFFFFu;
+    mag >>= 16;
+    if (lost) mag |= 1u;
+    reduced = 1;
+  }
+  const float hi = (float)(int32_t)(mag >> 24);
+  const float lo = (float)(int32_t)(mag & 0xFFFFFFu);
+  float r = hi * 16777216.0f + lo;
+  if (reduced) r = r * 65536.0f;
+  return neg ? -r : r;
+}
+
+/* checks/numerics_int15.mojo:166-172 dequant_int15_pinned (W-7). */
+static inline float q15_dequant(int64_t acc, int64_t e_sum) {
+  return ftz(orc_q15_i64_to_f32(acc) * pow2_f32(e_sum));
+}
+
+/* gemm/host/gemm_int15_oracle.mojo:116-131 quantize_rows_int15 and :160-168 split_int15: per row
+ * the int8i32 absmax, its W-1 exponent, the W-2 codes, written as the two planes. */
+void orc_q15_quantize_rows(int8_t* hi, int8_t* lo, int32_t* exps, const float* x, int64_t rows, int64_t cols) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    float best = 0.0f;
+    for (int64_t c = 0; c < cols; ++c) {
+      float v = ftz(x[r * cols + c]);
+      if (v < 0.0f) v = -v;
+      if (v > best) best = v;
+    }
+    const int e = orc_q15_row_exponent(best);
+    exps[r] = e;
+    for (int64_t c = 0; c < cols; ++c) {
+      const int16_t q = q15_value(x[r * cols + c], e);
+      hi[r * cols + c] = q15_hi(q);
+      lo[r * cols + c] = q15_lo(q);
+    }
+  }
+}
+
+/* gemm/host/gemm_int15_oracle.mojo:147-157 dequantize_rows_int15 with :170-176 join_int15:
+ * ftz(f32(hi * 128 + lo) * 2^e) through the W-6/W-7 seam. */
+void orc_q15_dequantize_rows(float* out, const int8_t* hi, const int8_t* lo, const int32_t* exps, int64_t rows,
+                             int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c) {
+      const int64_t q = (int64_t)hi[r * cols + c] * 128 + (int64_t)lo[r * cols + c];
+      out[r * cols + c] = q15_dequant(q, exps[r]);
+    }
+}
+
+/* gemm/host/gemm_int15_oracle.mojo:179-189 int15_dot_cell and :232-270 gemm_int15_oracle, the
+ * FLAT definition: codes joined from the planes, each product in Int32, the sum in Int64 (p
+ * ascending), then W-6/W-7. */
+void orc_q15_gemm(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
+                  const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      int64_t acc = 0;
+      for (int64_t p = 0; p < k; ++p) {
+        const int32_t qa = (int32_t)ah[i * k + p] * 128 + (int32_t)al[i * k + p];
+        const int32_t qb = (int32_t)bh[j * k + p] * 128 + (int32_t)bl[j * k + p];
+        acc += (int64_t)(qa * qb);
+      }
+      c[i * n + j] = q15_dequant(acc, (int64_t)ea[i] + (int64_t)eb[j]);
     }
 }
 

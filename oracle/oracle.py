@@ -49,6 +49,11 @@ def lib():
         L.orc_q8_quantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_quantize_rows.restype = None
         L.orc_q8_dequantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_dequantize_rows.restype = None
         L.orc_q8_gemm.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q8_gemm.restype = None
+        L.orc_q15_i64_to_f32.argtypes = [i64]; L.orc_q15_i64_to_f32.restype = f32
+        L.orc_q15_row_exponent.argtypes = [f32]; L.orc_q15_row_exponent.restype = c_int
+        L.orc_q15_quantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_quantize_rows.restype = None
+        L.orc_q15_dequantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_dequantize_rows.restype = None
+        L.orc_q15_gemm.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q15_gemm.restype = None
         L.orc_card_fill.argtypes = [vp, i64, i64]; L.orc_card_fill.restype = None
         L.orc_ftz.argtypes = [f32]; L.orc_ftz.restype = f32
         L.orc_fma.argtypes = [f32, f32, f32]; L.orc_fma.restype = f32
@@ -228,3 +233,49 @@ def q8_i32_to_f32(v):
 
 def q8_row_exponent(absmax):
     return lib().orc_q8_row_exponent(float(absmax))
+
+
+# ---- profile mojolearn.identical.gemm.int15i64.v1 (contract section 6, W-1..W-7)
+
+INT15_MAX_K = 65536
+
+
+def q15_quantize(x):
+    """(hi int8, lo int8, exponents int32): W-1/W-2 codes as W-3 planes, code = hi * 128 + lo."""
+    x = _f32c(x)
+    rows, cols = x.shape
+    hi = np.empty((rows, cols), np.int8)
+    lo = np.empty((rows, cols), np.int8)
+    exps = np.empty(rows, np.int32)
+    lib().orc_q15_quantize_rows(_p(hi), _p(lo), _p(exps), _p(x), rows, cols)
+    return hi, lo, exps
+
+
+def q15_dequantize(hi, lo, exps):
+    hi = np.ascontiguousarray(hi, dtype=np.int8)
+    lo = np.ascontiguousarray(lo, dtype=np.int8)
+    exps = np.ascontiguousarray(exps, dtype=np.int32)
+    rows, cols = hi.shape
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_q15_dequantize_rows(_p(out), _p(hi), _p(lo), _p(exps), rows, cols)
+    return out
+
+
+def q15_gemm(ah, al, ea, bh, bl, eb):
+    """C = a . b^T (OP_NT) as int15i64.v1: the exact Int64 sum of code products, W-6, W-7."""
+    ah, al, bh, bl = (np.ascontiguousarray(t, dtype=np.int8) for t in (ah, al, bh, bl))
+    ea = np.ascontiguousarray(ea, dtype=np.int32)
+    eb = np.ascontiguousarray(eb, dtype=np.int32)
+    (m, k), (n, kb) = ah.shape, bh.shape
+    assert k == kb and al.shape == ah.shape and bl.shape == bh.shape and ea.size == m and eb.size == n
+    c = np.empty((m, n), np.float32)
+    lib().orc_q15_gemm(_p(c), _p(ah), _p(al), _p(ea), _p(bh), _p(bl), _p(eb), m, n, k)
+    return c
+
+
+def q15_i64_to_f32(v):
+    return lib().orc_q15_i64_to_f32(int(v))
+
+
+def q15_row_exponent(absmax):
+    return lib().orc_q15_row_exponent(float(absmax))

@@ -12,7 +12,7 @@ Sources:
   bench/results/e1g/2026-09-17_203449-nvidia-refregen-par-lanes-b/remote/nvidia.card
       NVIDIA device card (byte-identical fields 2-5 to the MI325X one)
   python/mojolearn/verify_reference/table.json
-      cells gemm-pinned/*, gemm-transposed/*, gemm-bf16/*, gemm-int8/*, lowbit-conversions/*
+      cells gemm-pinned/*, gemm-transposed/*, gemm-bf16/*, gemm-int8/*, gemm-int15/*, lowbit-conversions/*
       (train column) and the
       fixture X hashes (tools/identity_break.py:1355-1382 hashing, :1434-1509 fixtures)
 """
@@ -39,7 +39,7 @@ def main():
     cells = {}
     for name, cell in table["cells"].items():
         lane = name.split("/")[0]
-        if lane in ("gemm-pinned", "gemm-transposed", "gemm-bf16", "gemm-int8", "lowbit-conversions"):
+        if lane in ("gemm-pinned", "gemm-transposed", "gemm-bf16", "gemm-int8", "gemm-int15", "lowbit-conversions"):
             cells[name] = {"train": cell["train"]["ref"]}
     out = {
         "source": "python/mojolearn/verify_reference/table.json",

@@ -70,3 +70,5 @@ def test_verify_gemm_lanes(oracle, kind):
     assert VL.train_hash(VL.lane_gemm_bf16(S.to_bf16, S.matmul_bf16, X)) == cells[f"gemm-bf16/{kind}"]["train"]
     lane = VL.lane_gemm_int8(S.quantize_int8, S.matmul_int8, S.dequantize_int8, X)
     assert VL.train_hash(lane) == cells[f"gemm-int8/{kind}"]["train"]
+    lane = VL.lane_gemm_int15(S.quantize_int15, S.matmul_int15, S.dequantize_int15, oracle.INT15_MAX_K, X)
+    assert VL.train_hash(lane) == cells[f"gemm-int15/{kind}"]["train"]

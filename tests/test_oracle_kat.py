@@ -266,3 +266,102 @@ def test_int8_gemm_at_max_k(oracle):
     got = oracle.q8_gemm(qa, e0, qb, e0)
     full = np.array([16129 * k], np.int64).astype(np.float32)[0]
     assert got[0, 0] == full and got[0, 1] == full and got[1, 0] == 0.0
+
+
+# ---- int15i64.v1 (contract section 6, W-1..W-7): numpy's own int64 -> float32 rounding, exact
+# rationals and integer matmul, none sharing a step with the oracle's spelling.
+
+def test_int15_i64_to_f32_is_round_half_even(oracle):
+    """W-6 on the ties and edges the contract plants, random values below and above 2^48 (the
+    sticky-bit branch), and the two ends of Int64."""
+    rng = np.random.default_rng(15)
+    vals = [0, 1, -1, 2 ** 24 + 1, 2 ** 24 + 3, -(2 ** 24 + 1), 2 ** 44, 2 ** 44 - 2 ** 31 + 2 ** 16,
+            2 ** 63 - 1, -(2 ** 63)]
+    for base in (2 ** 40 + 2 ** 16, 2 ** 40 + 3 * 2 ** 16, 2 ** 48, 2 ** 48 + 2 ** 24, 2 ** 48 + 3 * 2 ** 24):
+        vals += [base - 1, base, base + 1, -base + 1, -base, -base - 1]
+    for bits in (30, 44, 47, 48, 55, 62):
+        vals += [int(v) for v in rng.integers(-(2 ** bits), 2 ** bits, 500, dtype=np.int64)]
+    for v in vals:
+        want = np.array([v], np.int64).astype(np.float32)[0]
+        got = np.float32(oracle.q15_i64_to_f32(v))
+        assert got.view(np.uint32) == want.view(np.uint32), v
+
+
+def test_int15_pieces_cover_every_code(oracle):
+    """W-3 on all 32767 codes: a row of the integers themselves has absmax 16383, so e = 0 and
+    the codes are the values; hi is the floor quotient, lo the floor remainder."""
+    c = np.arange(-16383, 16384, dtype=np.int64)
+    hi, lo, e = oracle.q15_quantize(c.astype(np.float32).reshape(1, -1))
+    assert e[0] == 0
+    assert np.array_equal(hi[0].astype(np.int64), np.floor_divide(c, 128))
+    assert np.array_equal(lo[0].astype(np.int64), np.mod(c, 128))
+    assert lo.min() >= 0 and hi.min() == -128 and hi.max() == 127
+    assert np.array_equal(hi[0].astype(np.int64) * 128 + lo[0], c)
+
+
+def test_int15_quantize_rule(oracle):
+    """W-1/W-2 by exact rationals: e = floor(log2 absmax) - 13, codes clamp(rne(x 2^-e), +-16383),
+    with rows built to hold ties and the 16383.5 -> 16384 -> 16383 clamp."""
+    from fractions import Fraction
+    rng = np.random.default_rng(16)
+    rows = []
+    for r in range(30):
+        scale = 2.0 ** int(rng.integers(-100, 100))
+        row = rng.integers(-32767, 32768, 48).astype(np.float64) / 2.0 * scale / 2 ** 13
+        row[0] = 16383.5 * scale / 2 ** 13 * (1 if r % 2 else -1)
+        rows.append(row)
+    x = np.array(rows, np.float32)
+    hi, lo, exps = oracle.q15_quantize(x)
+    codes = hi.astype(np.int64) * 128 + lo
+    for i in range(x.shape[0]):
+        absmax = np.max(np.abs(x[i].astype(np.float64)))
+        e = int(np.frexp(absmax)[1]) - 1 - 13
+        assert exps[i] == e
+        for j in range(x.shape[1]):
+            q = max(-16383, min(16383, round(Fraction(float(x[i, j])) * Fraction(2) ** -e)))
+            assert codes[i, j] == q, (i, j)
+
+
+def test_int15_quantize_specials(oracle):
+    """A NaN codes to 0 before and after the scaling (a zero of a row whose 2^-e is infinite);
+    an infinity codes to +-16383 and sets the row exponent from its field (128 - 13)."""
+    x = np.array([[np.nan, 1.0, -0.5, 0.0],
+                  [np.inf, 1.0, -np.inf, 0.0],
+                  [2.0 ** -120, -(2.0 ** -121), 0.0, -0.0]], np.float32)
+    hi, lo, exps = oracle.q15_quantize(x)
+    codes = hi.astype(np.int64) * 128 + lo
+    assert list(exps) == [-13, 115, -133]
+    assert list(codes[0]) == [0, 8192, -4096, 0]
+    assert list(codes[1]) == [16383, 0, -16383, 0]
+    assert list(codes[2]) == [16383, -16383, 0, 0]
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 5, 1), (6, 4, 200), (4, 7, 4097)])
+def test_int15_gemm_exact(oracle, m, n, k):
+    """W-5..W-7: the exact integer dot product (numpy int64), rounded once to float32, scaled by
+    an exact power of two and flushed; exponent sums past both ends."""
+    rng = np.random.default_rng(m * 100 + k)
+    qa = rng.integers(-16383, 16384, (m, k)).astype(np.int64)
+    qb = rng.integers(-16383, 16384, (n, k)).astype(np.int64)
+    ea = rng.integers(-60, 60, m).astype(np.int32)
+    eb = rng.integers(-60, 60, n).astype(np.int32)
+    ea[0], eb[0] = -140, 10
+    planes = lambda q: ((q >> 7).astype(np.int8), (q & 127).astype(np.int8))
+    ah, al = planes(qa)
+    bh, bl = planes(qb)
+    got = oracle.q15_gemm(ah, al, ea, bh, bl, eb)
+    f = (qa @ qb.T).astype(np.float32).astype(np.float64)
+    es = ea[:, None].astype(np.int64) + eb[None, :].astype(np.int64)
+    want = _ftz32(np.where(es < -126, f * 0.0, np.ldexp(f, es)).astype(np.float32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_int15_gemm_at_max_k(oracle):
+    """k = 65536 with the code -16383 on both operands (hi = -128): the sum 16383^2 * 2^16 is
+    exact in Int64 and rounds once."""
+    k = 65536
+    ah = np.full((1, k), -128, np.int8)
+    al = np.full((1, k), 1, np.int8)
+    e0 = np.zeros(1, np.int32)
+    got = oracle.q15_gemm(ah, al, e0, ah, al, e0)
+    assert got[0, 0] == np.array([16383 * 16383 * k], np.int64).astype(np.float32)[0]

@@ -2,7 +2,8 @@
 
 Fixtures: tools/identity_break.py:1393 (N, D = 20000, 16) and :1414-1485 (`fixture`,
 `_hashed_uniform`).  Hashes: `_h` / `_train_hash` (:1355-1382).  Lanes: gemm-pinned
-(:2984-2995), gemm-transposed (:5880-5890), gemm-bf16 (:3825-3836), gemm-int8 (:3839-3849).  The recorded
+(:2984-2995), gemm-transposed (:5880-5890), gemm-bf16 (:3825-3836), gemm-int8 (:3839-3849),
+gemm-int15 (:3852-3879).  The recorded
 `train` hashes are in tests/golden/verify_gemm_cells.json (from
 python/mojolearn/verify_reference/table.json).
 
@@ -127,6 +128,29 @@ def lane_gemm_int8(quantize_int8, matmul_int8, dequantize_int8, X):
                 product=h(np.asarray(c)), dequant=h(np.asarray(dequantize_int8(qb, eb))))
 
 
+def lane_gemm_int15(quantize_int15, matmul_int15, dequantize_int15, int15_max_k, X):
+    """int15i64.v1 on the same slices: the planes and exponents, the product from the planes
+    and from the float32 operands (recorded as a number `same`), whether k above the
+    profile's maximum is refused by name, and a dequantization."""
+    a = np.ascontiguousarray(X[:256]).astype(np.float32)
+    b = np.ascontiguousarray(X[256:256 + 128]).astype(np.float32)
+    ah, al, ea = quantize_int15(a)
+    bh, bl, eb = quantize_int15(b)
+    c = np.asarray(matmul_int15((ah, al, ea), (bh, bl, eb)))
+    c1 = np.asarray(matmul_int15(a, b))
+    same = np.array([int(c.tobytes() == c1.tobytes())], dtype=np.int32)
+    wide = np.zeros((1, int15_max_k + 1), dtype=np.float32)
+    try:
+        matmul_int15(wide, wide)
+        refused = False
+    except Exception as exc:  # noqa: BLE001 -- the lane records a refusal as a number
+        refused = "65536" in str(exc)
+    refuses = np.array([int(refused)], dtype=np.int32)
+    return dict(planes=h(np.asarray(ah), np.asarray(al), np.asarray(bh), np.asarray(bl)),
+                exps=h(np.asarray(ea), np.asarray(eb)), product=h(c), onecall=h(c1), flags=h(same, refuses),
+                dequant=h(np.asarray(dequantize_int15(bh, bl, eb))))
+
+
 class OracleSurface:
     """The three surface calls the lanes need, answered by the CPU oracle."""
 
@@ -155,3 +179,17 @@ class OracleSurface:
         qa, ea = a if isinstance(a, tuple) else self.O.q8_quantize(a)
         qb, eb = b if isinstance(b, tuple) else self.O.q8_quantize(b)
         return self.O.nan_canon(self.O.q8_gemm(qa, ea, qb, eb))
+
+    def quantize_int15(self, x):
+        return self.O.q15_quantize(x)
+
+    def dequantize_int15(self, hi, lo, exps):
+        return self.O.nan_canon(self.O.q15_dequantize(hi, lo, exps))
+
+    def matmul_int15(self, a, b):
+        ah, al, ea = a if isinstance(a, tuple) else self.O.q15_quantize(a)
+        bh, bl, eb = b if isinstance(b, tuple) else self.O.q15_quantize(b)
+        k = np.asarray(ah).shape[1]
+        if k > self.O.INT15_MAX_K:
+            raise ValueError(f"matmul_int15: k={k} is above {self.O.INT15_MAX_K}")
+        return self.O.nan_canon(self.O.q15_gemm(ah, al, ea, bh, bl, eb))
