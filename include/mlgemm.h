@@ -49,7 +49,14 @@ typedef void (*mlg_sink_t)(int64_t ctx, int64_t utf8_ptr, int64_t len);
  *                                                                       (gemm/linalg_native.mojo:258-321)
  *   3   [codes_i8, exps_i32, x]     [rows, cols]               rows*cols quantize_int8 (L-3, L-4; :323-357)
  *   4   [y_f32, codes_i8, exps_i32] [rows, cols]               rows*cols dequantize_int8 (L-6; :359-393)
- * Ops 5-7 and 10 (int15i64 profile, from_f16) are refused by name.
+ *   5   [c, ah, al, ea, bh, bl, eb] [m, n, k]                  m*n      gemm_int15, profile int15i64.v1,
+ *                                                                       OP_NT: two int8 planes per operand
+ *                                                                       (code = hi*128 + lo), one int32
+ *                                                                       exponent per row; k <= 65536
+ *                                                                       (gemm/linalg_native.mojo:395-442)
+ *   6   [hi, lo, exps, x]           [rows, cols]               rows*cols quantize_int15 (W-1..W-3; :444-476)
+ *   7   [y, hi, lo, exps]           [rows, cols]               rows*cols dequantize_int15 (W-6, W-7; :478-510)
+ *  10   [f32_out, f16_bits]         [count]                    count    from_f16, exact (:564-576)
  */
 int64_t linalg_native_v1(int64_t op, int64_t addrs, int64_t n_addrs, int64_t ints, int64_t n_ints,
                          int64_t floats, int64_t n_floats, int64_t result, int64_t err_ctx,
@@ -126,6 +133,32 @@ int mlg_gemm_int8i32(float* c, const int8_t* qa, const int32_t* ea, const int8_t
 int64_t mlg_gemm_int8i32_workspace_bytes(const int8_t* qa, const int8_t* qb, int64_t m, int64_t n, int64_t k);
 int mlg_gemm_int8i32_ws(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
                         int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* IEEE float16 bits to float32, exact, NaN payloads kept (gemm/f16_widen.mojo:12-37). */
+int mlg_f16_widen(float* out, const uint16_t* in, int64_t count, void* stream);
+
+/* Profile mojolearn.identical.gemm.int15i64.v1 on device buffers (gemm/IDENTICAL_LOWBIT_CONTRACT.md
+ * section 6, W-1..W-7; the reference's device entries for gemm_int15 / quantize_int15 /
+ * dequantize_int15, gemm/linalg_native.mojo:395-510).  A code c in [-16383, 16383] is kept as two
+ * int8 planes, hi = floor(c / 128) and lo = c mod 128.
+ * quantize: per row e = floor(log2 absmax) - 13 (0 for an all-zero row), c = clamp(rne(ftz(x) *
+ *   2^-e), -16383, 16383), a NaN coding to 0 before and after the scaling.
+ * dequantize: out = ftz(f32(c) * 2^e) per row.
+ * gemm: OP_NT, C[i][j] = ftz(f32(sum_p ca[i][p] cb[j][p]) * 2^(ea[i] + eb[j])), the sum exact in Int64
+ *   (three Int32 plane sums, HH 2^14 + MID 2^7 + LL) and converted by W-6's pinned split;
+ *   1 <= k <= 65536.  Workspace as for mlg_gemm_int8i32 (repacks of planes whose rows are not a
+ *   multiple of 64 codes or 16-byte aligned; Int32 partial sums when k is split). */
+int mlg_int15_quantize(int8_t* hi, int8_t* lo, int32_t* exponents, const float* x, int64_t rows, int64_t cols,
+                       void* stream);
+int mlg_int15_dequantize(float* out, const int8_t* hi, const int8_t* lo, const int32_t* exponents, int64_t rows,
+                         int64_t cols, void* stream);
+int mlg_gemm_int15i64(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
+                      const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k, void* stream);
+int64_t mlg_gemm_int15i64_workspace_bytes(const int8_t* ah, const int8_t* al, const int8_t* bh, const int8_t* bl,
+                                          int64_t m, int64_t n, int64_t k);
+int mlg_gemm_int15i64_ws(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
+                         const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 
 /* The message of the calling thread's last failed mlg_* call ("" if none). */
 const char* mlg_last_error(void);

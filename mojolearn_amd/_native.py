@@ -57,6 +57,18 @@ def lib():
         L.mlg_gemm_int8i32_workspace_bytes.restype = i64
         L.mlg_gemm_int8i32_ws.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp]
         L.mlg_gemm_int8i32_ws.restype = ctypes.c_int
+        L.mlg_f16_widen.argtypes = [vp, vp, i64, vp]
+        L.mlg_f16_widen.restype = ctypes.c_int
+        L.mlg_int15_quantize.argtypes = [vp, vp, vp, vp, i64, i64, vp]
+        L.mlg_int15_quantize.restype = ctypes.c_int
+        L.mlg_int15_dequantize.argtypes = [vp, vp, vp, vp, i64, i64, vp]
+        L.mlg_int15_dequantize.restype = ctypes.c_int
+        L.mlg_gemm_int15i64.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp]
+        L.mlg_gemm_int15i64.restype = ctypes.c_int
+        L.mlg_gemm_int15i64_workspace_bytes.argtypes = [vp, vp, vp, vp, i64, i64, i64]
+        L.mlg_gemm_int15i64_workspace_bytes.restype = i64
+        L.mlg_gemm_int15i64_ws.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp]
+        L.mlg_gemm_int15i64_ws.restype = ctypes.c_int
         L.mlg_last_error.argtypes = []
         L.mlg_last_error.restype = ctypes.c_char_p
         for name in ("mlg_numeric_mode", "mlg_profile_version", "mlg_lowbit_profile_version"):

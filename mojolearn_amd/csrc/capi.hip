@@ -155,7 +155,7 @@ struct DeviceBuf {
 };
 
 struct HostPool {
-  DeviceBuf c, a, b, x, y, w;
+  DeviceBuf c, a, b, x, y, w, a2, b2;
   hipStream_t stream = nullptr;
 };
 
@@ -184,7 +184,7 @@ struct Lease {
       g_pool_busy.store(0);
     } else {
       fresh.c.release(); fresh.a.release(); fresh.b.release(); fresh.x.release(); fresh.y.release();
-      fresh.w.release();
+      fresh.w.release(); fresh.a2.release(); fresh.b2.release();
       if (fresh.stream) (void)hipStreamDestroy(fresh.stream);
     }
   }
@@ -238,6 +238,22 @@ int64_t host_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr
   down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
   hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
   return m * n;
+}
+
+// from_f16 (gemm/linalg_native.mojo:564-576): float16 bits to float32.
+int64_t host_from_f16(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr) {
+  if (pr.size() != 1) throw Fail("from_f16: params must contain 1 value (count)");
+  const int64_t count = pr[0];
+  if (count <= 0) throw Fail("from_f16: count must be positive, got " + std::to_string(count));
+  Lease lease;
+  HostPool& P = *lease.pool;
+  float* dout = (float*)P.c.get((size_t)count * 4);
+  uint16_t* din = (uint16_t*)P.a.get((size_t)count * 2);
+  up(din, (const void*)ad[1], (size_t)count * 2, P.stream);
+  hip_check(mlg::run_f16_widen(dout, din, count, P.stream), "from_f16 launch");
+  down((void*)ad[0], dout, (size_t)count * 4, P.stream);
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  return count;
 }
 
 int64_t host_convert(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr, bool narrow) {
@@ -314,6 +330,69 @@ int64_t host_q8_convert(const std::vector<int64_t>& ad, const std::vector<int64_
   return rows * cols;
 }
 
+// ---- profile int15i64.v1 on host pointers (gemm/linalg_native.mojo:395-510; refusals :114-121)
+int64_t host_q15_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr) {
+  if (pr.size() != 3) throw Fail("gemm_int15: params must contain 3 values (m, n, k), got " + std::to_string(pr.size()));
+  const int64_t m = pr[0], n = pr[1], k = pr[2];
+  if (m <= 0 || n <= 0 || k <= 0)
+    throw Fail("gemm_int15: m, n and k must all be positive, got m=" + std::to_string(m) + " n=" +
+               std::to_string(n) + " k=" + std::to_string(k));
+  if (k > mlg::INT15_MAX_K)
+    throw Fail("gemm_int15: k must be at most " + std::to_string(mlg::INT15_MAX_K) + " (contract W-4), got " +
+               std::to_string(k));
+  Lease lease;  // addrs: c, a hi, a lo, a exponents, b hi, b lo, b exponents
+  HostPool& P = *lease.pool;
+  float* dc = (float*)P.c.get((size_t)(m * n) * 4);
+  int8_t* dah = (int8_t*)P.a.get((size_t)(m * k));
+  int8_t* dal = (int8_t*)P.a2.get((size_t)(m * k));
+  int8_t* dbh = (int8_t*)P.b.get((size_t)(n * k));
+  int8_t* dbl = (int8_t*)P.b2.get((size_t)(n * k));
+  int32_t* dea = (int32_t*)P.x.get((size_t)m * 4);
+  int32_t* deb = (int32_t*)P.y.get((size_t)n * 4);
+  up(dah, (const void*)ad[1], (size_t)(m * k), P.stream);
+  up(dal, (const void*)ad[2], (size_t)(m * k), P.stream);
+  up(dea, (const void*)ad[3], (size_t)m * 4, P.stream);
+  up(dbh, (const void*)ad[4], (size_t)(n * k), P.stream);
+  up(dbl, (const void*)ad[5], (size_t)(n * k), P.stream);
+  up(deb, (const void*)ad[6], (size_t)n * 4, P.stream);
+  const int cus = num_cus_of_current_device();
+  const int64_t wsb = mlg::q15_workspace_bytes(dah, dal, dbh, dbl, m, n, k, cus);
+  void* dws = wsb > 0 ? P.w.get((size_t)wsb) : nullptr;
+  hip_check(mlg::run_q15_gemm(dc, dah, dal, dea, dbh, dbl, deb, m, n, k, dws, cus, P.stream), "gemm_int15 launch");
+  down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  return m * n;
+}
+
+int64_t host_q15_convert(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr, bool quantize) {
+  const char* who = quantize ? "quantize_int15" : "dequantize_int15";
+  if (pr.size() != 2) throw Fail(std::string(who) + ": params must contain 2 values (rows, cols), got " + std::to_string(pr.size()));
+  const int64_t rows = pr[0], cols = pr[1];
+  if (rows <= 0 || cols <= 0)
+    throw Fail(std::string(who) + ": rows and cols must be positive, got " + std::to_string(rows) + " x " + std::to_string(cols));
+  Lease lease;
+  HostPool& P = *lease.pool;
+  float* df = (float*)P.c.get((size_t)(rows * cols) * 4);
+  int8_t* dh = (int8_t*)P.a.get((size_t)(rows * cols));
+  int8_t* dl = (int8_t*)P.a2.get((size_t)(rows * cols));
+  int32_t* de = (int32_t*)P.x.get((size_t)rows * 4);
+  if (quantize) {  // addrs [hi, lo, exponents, x]
+    up(df, (const void*)ad[3], (size_t)(rows * cols) * 4, P.stream);
+    hip_check(mlg::run_q15_quantize(dh, dl, de, df, rows, cols, P.stream), "quantize_int15 launch");
+    down((void*)ad[0], dh, (size_t)(rows * cols), P.stream);
+    down((void*)ad[1], dl, (size_t)(rows * cols), P.stream);
+    down((void*)ad[2], de, (size_t)rows * 4, P.stream);
+  } else {  // addrs [y, hi, lo, exponents]
+    up(dh, (const void*)ad[1], (size_t)(rows * cols), P.stream);
+    up(dl, (const void*)ad[2], (size_t)(rows * cols), P.stream);
+    up(de, (const void*)ad[3], (size_t)rows * 4, P.stream);
+    hip_check(mlg::run_q15_dequantize(df, dh, dl, de, rows, cols, P.stream), "dequantize_int15 launch");
+    down((void*)ad[0], df, (size_t)(rows * cols) * 4, P.stream);
+  }
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  return rows * cols;
+}
+
 std::vector<int64_t> words(int64_t addr, int64_t n) {
   if (n < 0 || (n > 0 && addr == 0)) throw Fail("linalg native ABI: invalid descriptor span");
   std::vector<int64_t> v((size_t)n);
@@ -364,9 +443,18 @@ int64_t native_operation(int64_t op, const std::vector<int64_t>& a, const std::v
     case 4:
       if (a.size() != 3) throw Fail("linalg native ABI: invalid dequantize_int8 address count");
       return host_q8_convert(a, p, false);
-    case 5: case 6: case 7: case 10:
-      throw Fail("linalg native ABI: operation " + std::to_string(op) +
-                 " (int15i64 profile, from_f16) is not part of this build");
+    case 5:
+      if (a.size() != 7) throw Fail("linalg native ABI: invalid gemm_int15 address count");
+      return host_q15_gemm(a, p);
+    case 6:
+      if (a.size() != 4) throw Fail("linalg native ABI: invalid quantize_int15 address count");
+      return host_q15_convert(a, p, true);
+    case 7:
+      if (a.size() != 4) throw Fail("linalg native ABI: invalid dequantize_int15 address count");
+      return host_q15_convert(a, p, false);
+    case 10:
+      if (a.size() != 2) throw Fail("linalg native ABI: invalid from_f16 address count");
+      return host_from_f16(a, p);
     default:
       throw Fail("linalg native ABI: unknown operation");
   }
@@ -528,6 +616,84 @@ int mlg_gemm_int8i32_ws(float* c, const int8_t* qa, const int32_t* ea, const int
     hip_check(mlg::run_q8_gemm(c, qa, ea, qb, eb, m, n, k, need > 0 ? workspace : nullptr, cus,
                                (hipStream_t)stream),
               "gemm_int8 launch");
+  });
+}
+
+int mlg_f16_widen(float* out, const uint16_t* in, int64_t count, void* stream) {
+  return guarded([&] { hip_check(mlg::run_f16_widen(out, in, count, (hipStream_t)stream), "from_f16 launch"); });
+}
+
+int mlg_int15_quantize(int8_t* hi, int8_t* lo, int32_t* exponents, const float* x, int64_t rows, int64_t cols,
+                       void* stream) {
+  return guarded([&] {
+    if (rows < 0 || cols < 0) throw Fail("quantize_int15: rows and cols must be >= 0");
+    if (rows > 0 && cols > 0 && (!hi || !lo || !exponents || !x)) throw Fail("quantize_int15: null pointer");
+    hip_check(mlg::run_q15_quantize(hi, lo, exponents, x, rows, cols, (hipStream_t)stream), "quantize_int15 launch");
+  });
+}
+
+int mlg_int15_dequantize(float* out, const int8_t* hi, const int8_t* lo, const int32_t* exponents, int64_t rows,
+                         int64_t cols, void* stream) {
+  return guarded([&] {
+    if (rows < 0 || cols < 0) throw Fail("dequantize_int15: rows and cols must be >= 0");
+    if (rows > 0 && cols > 0 && (!out || !hi || !lo || !exponents)) throw Fail("dequantize_int15: null pointer");
+    hip_check(mlg::run_q15_dequantize(out, hi, lo, exponents, rows, cols, (hipStream_t)stream),
+              "dequantize_int15 launch");
+  });
+}
+
+static void check_q15_args(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
+                           const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0)
+    throw Fail("gemm_int15: m, n and k must all be positive, got m=" + std::to_string(m) + " n=" +
+               std::to_string(n) + " k=" + std::to_string(k));
+  if (k > mlg::INT15_MAX_K)
+    throw Fail("gemm_int15: k must be at most " + std::to_string(mlg::INT15_MAX_K) + " (contract W-4), got " +
+               std::to_string(k));
+  if (!c || !ah || !al || !ea || !bh || !bl || !eb) throw Fail("gemm_int15: null operand pointer");
+}
+
+int mlg_gemm_int15i64(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
+                      const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k, void* stream) {
+  return guarded([&] {
+    check_q15_args(c, ah, al, ea, bh, bl, eb, m, n, k);
+    hipStream_t s = (hipStream_t)stream;
+    const int cus = num_cus_of_current_device();
+    const int64_t wsb = mlg::q15_workspace_bytes(ah, al, bh, bl, m, n, k, cus);
+    void* ws = nullptr;
+    if (wsb > 0) hip_check(hipMallocAsync(&ws, (size_t)wsb, s), "hipMallocAsync");
+    hipError_t e = mlg::run_q15_gemm(c, ah, al, ea, bh, bl, eb, m, n, k, ws, cus, s);
+    if (ws) {
+      hipError_t f = hipFreeAsync(ws, s);
+      if (e == hipSuccess) e = f;
+    }
+    hip_check(e, "gemm_int15 launch");
+  });
+}
+
+int64_t mlg_gemm_int15i64_workspace_bytes(const int8_t* ah, const int8_t* al, const int8_t* bh, const int8_t* bl,
+                                          int64_t m, int64_t n, int64_t k) {
+  int64_t r = -1;
+  const int rc = guarded([&] {
+    if (m <= 0 || n <= 0 || k <= 0 || k > mlg::INT15_MAX_K) throw Fail("gemm_int15: invalid shape");
+    r = mlg::q15_workspace_bytes(ah, al, bh, bl, m, n, k, num_cus_of_current_device());
+  });
+  return rc == 0 ? r : -1;
+}
+
+int mlg_gemm_int15i64_ws(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
+                         const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    check_q15_args(c, ah, al, ea, bh, bl, eb, m, n, k);
+    const int cus = num_cus_of_current_device();
+    const int64_t need = mlg::q15_workspace_bytes(ah, al, bh, bl, m, n, k, cus);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+      throw Fail("gemm_int15: workspace of " + std::to_string(workspace_bytes) + " bytes, this product needs " +
+                 std::to_string(need));
+    hip_check(mlg::run_q15_gemm(c, ah, al, ea, bh, bl, eb, m, n, k, need > 0 ? workspace : nullptr, cus,
+                                (hipStream_t)stream),
+              "gemm_int15 launch");
   });
 }
 

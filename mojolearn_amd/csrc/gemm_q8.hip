@@ -1,6 +1,6 @@
-// gfx950 kernels of the profile mojolearn.identical.gemm.int8i32.v1
-// (gemm/IDENTICAL_LOWBIT_CONTRACT.md L-3..L-7): the row quantizer, the dequantizer and the OP_NT
-// product on the integer matrix unit.
+// gfx950 kernels of the integer profiles mojolearn.identical.gemm.int8i32.v1
+// (gemm/IDENTICAL_LOWBIT_CONTRACT.md L-3..L-7) and int15i64.v1 (section 6, W-1..W-7): the row
+// quantizers, the dequantizers and the OP_NT products on the integer matrix unit.
 //
 // The product's only arithmetic before the store is an integer sum of int8 x int8 products in an
 // Int32 that cannot overflow (k <= 131072), so the order in which the matrix unit adds them is
@@ -252,6 +252,259 @@ __global__ void q8_repack_kernel(int8_t* dst, const int8_t* src, int64_t rows, i
 }
 
 // ---------------------------------------------------------------------------
+// Profile mojolearn.identical.gemm.int15i64.v1 (contract section 6, W-1..W-7): codes in
+// [-16383, 16383] kept as two int8 planes, hi = floor(c / 128) in [-128, 127] and lo = c mod 128
+// in [0, 127].  The product runs the planes on the same integer matrix unit: three exact Int32
+// sums per cell, HH = sum ah bh, MID = sum (ah bl + al bh) (one accumulator, exact for
+// k <= 66052) and LL = sum al bl, recombined in Int64 as HH 2^14 + MID 2^7 + LL (W-4, W-5), then
+// W-6's pinned conversion and W-7's scale.  All three sums are integer, so their order is
+// scheduling, as for int8i32.
+
+constexpr int64_t INT15_MAX_K_DEV = 65536;
+
+// checks/numerics_int15.mojo:123-163 i64_to_f32_pinned (W-6): two exact 24-bit conversions and
+// one IEEE addition below 2^48; above, the low sixteen bits folded into a sticky bit and an
+// exact scaling by 2^16.
+__device__ __forceinline__ float q15_i64_to_f32(int64_t v) {
+  const bool neg = v < 0;
+  uint64_t mag = (uint64_t)v;
+  if (neg) mag = (uint64_t)0 - mag;
+  bool reduced = false;
+  if (mag >= ((uint64_t)1 << 48)) {
+    const uint64_t lost = mag & 0xFFFFu;
+    mag >>= 16;
+    if (lost) mag |= 1u;
+    reduced = true;
+  }
+  const float hi = (float)(int32_t)(mag >> 24);
+  const float lo = (float)(int32_t)(mag & 0xFFFFFFu);
+  float r = hi * 16777216.0f + lo;
+  if (reduced) r = r * 65536.0f;
+  return neg ? -r : r;
+}
+
+// checks/numerics_int15.mojo:166-172 (W-7), then the store's NaN canonicalisation.
+__device__ __forceinline__ float q15_dequant(int64_t acc, int64_t e_sum) {
+  return store_word(q8_ftz(q15_i64_to_f32(acc) * q8_pow2(e_sum)));
+}
+
+// checks/numerics_int15.mojo:66-93 quantize_int15_value (W-2): a NaN codes to 0 before the
+// scaling and after it.
+__device__ __forceinline__ int q15_code(float x, int e) {
+  if (x != x) return 0;
+  const float s = q8_ftz(q8_ftz(x) * q8_pow2(-(int64_t)e));
+  if (s != s) return 0;
+  const float magic = 12582912.0f;  // checks/numerics.mojo:1577-1586 f32_round_half_even
+  float r = s >= 0.f ? (s + magic) - magic : (s - magic) + magic;
+  if (r > 16383.f) r = 16383.f;
+  if (r < -16383.f) r = -16383.f;
+  return (int)r;
+}
+
+// W-1..W-3 per row (gemm/host/gemm_int15_oracle.mojo:116-131, :160-168): int8i32's absmax,
+// e = floor(log2 absmax) - 13, the codes straight to their planes.
+__global__ void __launch_bounds__(Q8_THREADS) q15_quantize_kernel(int8_t* hi, int8_t* lo, int32_t* exps,
+                                                                  const float* x, int64_t cols) {
+  __shared__ float wbest[Q8_THREADS / 64];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * cols;
+  float best = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += Q8_THREADS) best = q8_absmax_step(best, xr[c]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(best, off, 64);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+  __syncthreads();
+  best = wbest[0];
+#pragma unroll
+  for (int w = 1; w < Q8_THREADS / 64; ++w) best = wbest[w] > best ? wbest[w] : best;
+  // checks/numerics_int15.mojo:54-63 int15_row_exponent
+  const float a = q8_ftz(best);
+  const int e = (a == 0.f || a != a) ? 0 : (int)((__float_as_uint(a) >> 23) & 0xFFu) - 127 - 13;
+  if (threadIdx.x == 0) exps[row] = e;
+  for (int64_t c = threadIdx.x; c < cols; c += Q8_THREADS) {
+    const int q = q15_code(xr[c], e);
+    hi[row * cols + c] = (int8_t)(q >> 7);   // int15_piece_hi: the arithmetic shift
+    lo[row * cols + c] = (int8_t)(q & 127);  // int15_piece_lo: the low seven bits
+  }
+}
+
+// gemm/host/gemm_int15_oracle.mojo:147-157 with :170-176: ftz(f32(hi * 128 + lo) * 2^e).
+__global__ void q15_dequantize_kernel(float* out, const int8_t* hi, const int8_t* lo, const int32_t* exps,
+                                      int64_t rows, int64_t cols) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * cols) return;
+  out[i] = q15_dequant((int64_t)hi[i] * 128 + (int64_t)lo[i], exps[i / cols]);
+}
+
+// W-5 and the store of one cell.
+__device__ __forceinline__ float q15_cell(int32_t hh, int32_t mid, int32_t ll, int64_t e_sum) {
+  const int64_t s = ((int64_t)hh << 14) + ((int64_t)mid << 7) + (int64_t)ll;
+  return q15_dequant(s, e_sum);
+}
+
+struct Q15Args {
+  float* c;
+  const void* ah;  // [m][pitch] planes (pitch a multiple of Q15_KS codes, zero codes past k)
+  const void* al;
+  const void* bh;  // [n][pitch]
+  const void* bl;
+  const int32_t* ea;
+  const int32_t* eb;
+  int64_t m, n, k;
+  int64_t pitch_words;
+  int64_t a_bytes, b_bytes;
+  int32_t* part;  // split k: [splits][3][m][n] Int32 partial sums (HH, MID, LL), else nullptr
+  int64_t sps;    // slices per split
+  int tiles_n;
+};
+
+constexpr int Q15_SK = KT / 2;        // words per row per slice: 64 codes
+constexpr int Q15_KS = Q15_SK * 4;    // codes per slice
+constexpr int Q15_PLANE = BM * Q15_SK * 4;  // bytes of one plane's slice: 8 KB
+
+// The four products of one 64-code slice.  Every row is stored at a pitch of whole slices with
+// zero codes past k (the host repacks otherwise), so no code past k reaches a product.
+__device__ __forceinline__ void q15_slice(v16i (&hh)[2], v16i (&mid)[2], v16i (&ll)[2], const char* lah,
+                                          const char* lal, const char* lbh, const char* lbl, int wr, int lane,
+                                          int bcol) {
+#pragma unroll
+  for (int q = 0; q < Q15_KS / 32; ++q) {
+    const int s = 8 * q + 4 * (lane >> 5);  // word offset of this lane's 16 codes in the row
+    const v4i bh4 = __builtin_bit_cast(v4i, read4<T_F32, true, Q15_SK>(lbh, bcol, s, 1.f));
+    const v4i bl4 = __builtin_bit_cast(v4i, read4<T_F32, true, Q15_SK>(lbl, bcol, s, 1.f));
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const int arow = wr * 64 + 32 * blk + (lane & 31);
+      const v4i ah4 = __builtin_bit_cast(v4i, read4<T_F32, true, Q15_SK>(lah, arow, s, 1.f));
+      const v4i al4 = __builtin_bit_cast(v4i, read4<T_F32, true, Q15_SK>(lal, arow, s, 1.f));
+      hh[blk] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah4, bh4, hh[blk], 0, 0, 0);
+      mid[blk] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah4, bl4, mid[blk], 0, 0, 0);
+      mid[blk] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al4, bh4, mid[blk], 0, 0, 0);
+      ll[blk] = __builtin_amdgcn_mfma_i32_32x32x32_i8(al4, bl4, ll[blk], 0, 0, 0);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(NTHREADS) q15_gemm_kernel(Q15Args g) {
+  __shared__ __attribute__((aligned(1024))) char lds0[4][Q15_PLANE];
+  __shared__ __attribute__((aligned(1024))) char lds1[4][Q15_PLANE];
+  __shared__ __attribute__((aligned(1024))) char lds2[4][Q15_PLANE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 2;
+  const int wc = wave & 3;
+  const int64_t i0 = (int64_t)(blockIdx.x / g.tiles_n) * BM;
+  const int64_t j0 = (int64_t)(blockIdx.x % g.tiles_n) * BN;
+  const int64_t nslices = (g.k + Q15_KS - 1) / Q15_KS;
+  const int64_t kt0 = (int64_t)blockIdx.y * g.sps;
+  const int64_t kt1 = kt0 + g.sps < nslices ? kt0 + g.sps : nslices;
+
+  DirectLoader<T_F32, true, Q15_SK> lah, lal, lbh, lbl;
+  lah.init(g.pitch_words, wave, lane);
+  lal.init(g.pitch_words, wave, lane);
+  lbh.init(g.pitch_words, wave, lane);
+  lbl.init(g.pitch_words, wave, lane);
+  constexpr int LPS = 4 * Slice<T_F32, true, Q15_SK>::PER_WAVE;
+  constexpr int WAIT_ONE_BEHIND = (LPS & 0xF) | ((LPS >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+#define MLG_Q15_ISSUE(BUF, KTI)                                                         \
+  do {                                                                                  \
+    lah.issue(BUF[0], g.ah, g.a_bytes, g.pitch_words, i0, (KTI) * Q15_SK, wave);        \
+    lal.issue(BUF[1], g.al, g.a_bytes, g.pitch_words, i0, (KTI) * Q15_SK, wave);        \
+    lbh.issue(BUF[2], g.bh, g.b_bytes, g.pitch_words, j0, (KTI) * Q15_SK, wave);        \
+    lbl.issue(BUF[3], g.bl, g.b_bytes, g.pitch_words, j0, (KTI) * Q15_SK, wave);        \
+  } while (0)
+  MLG_Q15_ISSUE(lds0, kt0);
+  MLG_Q15_ISSUE(lds1, kt0 + 1);
+
+  const int bcol = wc * 32 + (lane & 31);
+  v16i hh[2], mid[2], ll[2];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) hh[blk][e] = mid[blk][e] = ll[blk][e] = 0;
+
+  __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND);
+  lds_barrier();
+
+#define MLG_Q15_STEP(CUR, FILL)                                                                    \
+  do {                                                                                             \
+    MLG_Q15_ISSUE(FILL, kt + 2);                                                                   \
+    q15_slice(hh, mid, ll, CUR[0], CUR[1], CUR[2], CUR[3], wr, lane, bcol);                        \
+    __builtin_amdgcn_s_waitcnt(WAIT_ONE_BEHIND);                                                   \
+    lds_barrier();                                                                                 \
+  } while (0)
+  // whole rotations of the three buffers, then the zero to two slices left (single entry
+  // and exit, so the accumulators keep their registers across the loop)
+  int64_t kt = kt0;
+  for (const int64_t kr = kt0 + (kt1 - kt0) / 3 * 3; kt < kr; kt += 3) {
+    MLG_Q15_STEP(lds0, lds2);
+    ++kt;
+    MLG_Q15_STEP(lds1, lds0);
+    ++kt;
+    MLG_Q15_STEP(lds2, lds1);
+    kt -= 2;
+  }
+  if (kt < kt1) {
+    MLG_Q15_STEP(lds0, lds2);
+    ++kt;
+    if (kt < kt1) MLG_Q15_STEP(lds1, lds0);
+  }
+#undef MLG_Q15_STEP
+#undef MLG_Q15_ISSUE
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load into LDS outlives the workgroup
+
+  const int64_t col = j0 + bcol;
+  if (col >= g.n) return;
+  if (g.part != nullptr) {  // split k: the three exact partial sums, folded by q15_reduce_kernel
+    int32_t* pr = g.part + (int64_t)blockIdx.y * 3 * g.m * g.n;
+    const int64_t mn = g.m * g.n;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = i0 + wr * 64 + 32 * blk + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+        if (row < g.m) {
+          pr[row * g.n + col] = hh[blk][r];
+          pr[mn + row * g.n + col] = mid[blk][r];
+          pr[2 * mn + row * g.n + col] = ll[blk][r];
+        }
+      }
+    }
+    return;
+  }
+  const int64_t eb = g.eb[col];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = i0 + wr * 64 + 32 * blk + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+      if (row < g.m) g.c[row * g.n + col] = q15_cell(hh[blk][r], mid[blk][r], ll[blk][r], (int64_t)g.ea[row] + eb);
+    }
+  }
+}
+
+// The split-k fold of the three sums (each exact in Int32 for k <= 65536, every running sum
+// bounded like the whole), then W-5..W-7.
+__global__ void q15_reduce_kernel(float* c, const int32_t* part, const int32_t* ea, const int32_t* eb, int64_t m,
+                                  int64_t n, int splits) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t mn = m * n;
+  if (i >= mn) return;
+  int32_t hh = 0, mid = 0, ll = 0;
+  for (int s = 0; s < splits; ++s) {
+    hh += part[(3 * s) * mn + i];
+    mid += part[(3 * s + 1) * mn + i];
+    ll += part[(3 * s + 2) * mn + i];
+  }
+  c[i] = q15_cell(hh, mid, ll, (int64_t)ea[i / n] + eb[i % n]);
+}
+
+// ---------------------------------------------------------------------------
 // host side
 
 static bool q8_in_place(const void* p, int64_t k) { return k % 16 == 0 && ((uintptr_t)p % 16u) == 0; }
@@ -259,12 +512,13 @@ static int64_t q8_pitch(int64_t k) { return (k + 15) / 16 * 16; }
 
 // Split k when the output tiles leave CUs idle (the skinny decode rows): about two workgroups
 // per CU, at least two slices per split, the partial sums capped at 64 MB.
-static int64_t q8_splits(int64_t m, int64_t n, int64_t k, int num_cus, int64_t* sps) {
+static int64_t q8_splits(int64_t m, int64_t n, int64_t k, int num_cus, int64_t* sps, int ks = Q8_KS,
+                         int64_t part_words = 1) {
   const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  const int64_t nslices = (k + Q8_KS - 1) / Q8_KS;
+  const int64_t nslices = (k + ks - 1) / ks;
   int64_t want = tiles >= num_cus ? 1 : (2 * (int64_t)num_cus + tiles - 1) / tiles;
   if (want > nslices / 2) want = nslices / 2;
-  while (want > 1 && want * m * n * 4 > (int64_t(64) << 20)) --want;
+  while (want > 1 && want * part_words * m * n * 4 > (int64_t(64) << 20)) --want;
   if (want < 1) want = 1;
   *sps = (nslices + want - 1) / want;
   return (nslices + *sps - 1) / *sps;
@@ -339,6 +593,86 @@ hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8
   if (e != hipSuccess || splits == 1) return e;
   hipLaunchKernelGGL(q8_reduce_kernel, dim3((unsigned)((m * n + 255) / 256)), dim3(256), 0, stream, c, part, ea, eb,
                      m, n, (int)splits);
+  return hipGetLastError();
+}
+
+
+hipError_t run_q15_quantize(int8_t* hi, int8_t* lo, int32_t* exps, const float* x, int64_t rows, int64_t cols,
+                            hipStream_t stream) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  hipLaunchKernelGGL(q15_quantize_kernel, dim3((unsigned)rows), dim3(Q8_THREADS), 0, stream, hi, lo, exps, x, cols);
+  return hipGetLastError();
+}
+
+hipError_t run_q15_dequantize(float* out, const int8_t* hi, const int8_t* lo, const int32_t* exps, int64_t rows,
+                              int64_t cols, hipStream_t stream) {
+  const int64_t total = rows * cols;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(q15_dequantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, out, hi,
+                     lo, exps, rows, cols);
+  return hipGetLastError();
+}
+
+// The product reads whole 64-code slices: planes whose rows are not a multiple of 64 codes, or
+// whose base is not 16-byte aligned, are repacked with zero codes to the next multiple.
+static bool q15_in_place(const void* p, int64_t k) { return k % Q15_KS == 0 && ((uintptr_t)p % 16u) == 0; }
+static int64_t q15_pitch(int64_t k) { return (k + Q15_KS - 1) / Q15_KS * Q15_KS; }
+
+int64_t q15_workspace_bytes(const void* ah, const void* al, const void* bh, const void* bl, int64_t m, int64_t n,
+                            int64_t k, int num_cus) {
+  int64_t bytes = 0;
+  if (!q15_in_place(ah, k) || !q15_in_place(al, k)) bytes += 2 * round256(m * q15_pitch(k));
+  if (!q15_in_place(bh, k) || !q15_in_place(bl, k)) bytes += 2 * round256(n * q15_pitch(k));
+  int64_t sps;
+  const int64_t splits = q8_splits(m, n, k, num_cus, &sps, Q15_KS, 3);
+  if (splits > 1) bytes += round256(splits * 3 * m * n * 4);
+  return bytes;
+}
+
+hipError_t run_q15_gemm(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
+                        const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k, void* ws, int num_cus,
+                        hipStream_t stream) {
+  if (m <= 0 || n <= 0 || k <= 0 || k > INT15_MAX_K_DEV) return hipErrorInvalidValue;
+  const int64_t pitch = q15_pitch(k);
+  if (32 * pitch + Q15_KS >= (int64_t(1) << 30)) return hipErrorInvalidValue;
+  char* wsp = static_cast<char*>(ws);
+  const void* pl[2][2] = {{ah, al}, {bh, bl}};
+  const int64_t rows[2] = {m, n};
+  for (int w = 0; w < 2; ++w) {
+    if (q15_in_place(pl[w][0], k) && q15_in_place(pl[w][1], k)) continue;
+    if (wsp == nullptr) return hipErrorInvalidValue;
+    const int64_t total = rows[w] * pitch;
+    for (int h = 0; h < 2; ++h) {
+      hipLaunchKernelGGL(q8_repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                         reinterpret_cast<int8_t*>(wsp), static_cast<const int8_t*>(pl[w][h]), rows[w], k, pitch);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      pl[w][h] = wsp;
+      wsp += round256(total);
+    }
+  }
+  int64_t sps;
+  const int64_t splits = q8_splits(m, n, k, num_cus, &sps, Q15_KS, 3);
+  int32_t* part = nullptr;
+  if (splits > 1) {
+    if (wsp == nullptr) return hipErrorInvalidValue;
+    part = reinterpret_cast<int32_t*>(wsp);
+  }
+  Q15Args g;
+  g.c = c; g.ah = pl[0][0]; g.al = pl[0][1]; g.bh = pl[1][0]; g.bl = pl[1][1]; g.ea = ea; g.eb = eb;
+  g.m = m; g.n = n; g.k = k;
+  g.pitch_words = pitch / 4;
+  g.a_bytes = m * pitch;
+  g.b_bytes = n * pitch;
+  g.part = part;
+  g.sps = sps;
+  const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  g.tiles_n = (int)tn;
+  hipLaunchKernelGGL(q15_gemm_kernel, dim3((unsigned)(tm * tn), (unsigned)splits), dim3(NTHREADS), 0, stream, g);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  hipLaunchKernelGGL(q15_reduce_kernel, dim3((unsigned)((m * n + 255) / 256)), dim3(256), 0, stream, c, part, ea,
+                     eb, m, n, (int)splits);
   return hipGetLastError();
 }
 

@@ -32,6 +32,8 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
 
 // Elementwise conversions used by the low-bit surface (to_bf16 / from_bf16).
 hipError_t run_bf16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream);
+// IEEE float16 bits -> float32, exact (gemm/f16_widen.mojo:12-37).
+hipError_t run_f16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream);
 hipError_t run_bf16_narrow(uint16_t* out, const float* in, int64_t count, hipStream_t stream);
 
 }  // namespace mlg

@@ -171,6 +171,38 @@ __global__ void bf16_narrow_kernel(uint16_t* out, const float* in, int64_t count
   out[i] = (uint16_t)((b + 0x7FFFu + lsb) >> 16);
 }
 
+// gemm/f16_widen.mojo:12-37 f16_bits_to_f32_bits: exact, integer operations only; a subnormal
+// float16 renormalized into a normal float32, every NaN keeping its sign and payload.
+__global__ void f16_widen_kernel(float* out, const uint16_t* in, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const uint32_t h = in[i];
+  const uint32_t s = (h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu;
+  uint32_t m = h & 0x03FFu;
+  uint32_t w;
+  if (e == 0u) {
+    if (m == 0u) {
+      w = s;
+    } else {
+      const uint32_t shift = (uint32_t)__builtin_clz(m) - 21u;  // shifts until bit 10 is set
+      m = (m << shift) & 0x03FFu;
+      w = s | ((113u - shift) << 23) | (m << 13);
+    }
+  } else if (e == 31u) {
+    w = s | 0x7F800000u | (m << 13);
+  } else {
+    w = s | ((e + 112u) << 23) | (m << 13);
+  }
+  out[i] = __uint_as_float(w);
+}
+
+hipError_t run_f16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(f16_widen_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, out, in, count);
+  return hipGetLastError();
+}
+
 hipError_t run_bf16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream) {
   if (count <= 0) return hipSuccess;
   hipLaunchKernelGGL(bf16_widen_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,

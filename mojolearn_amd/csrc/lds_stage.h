@@ -6,21 +6,21 @@
 
 namespace mlg {
 
-// One staged slice (BM indices x KT steps) of an operand of element type T, as
-// NCH = BM*KT*bytes/16 chunks of 16 bytes, chunk position p loaded by lane p % 64 of
+// One staged slice (BM indices x SK steps; SK = KT unless a kernel says otherwise) of an
+// operand of element type T, as NCH = BM*SK*bytes/16 chunks of 16 bytes, chunk position p loaded by lane p % 64 of
 // load instruction p / 64 (a load instruction fills 1 KB of LDS, lane L at L*16).
 //  * index-major (the operand stores k contiguously: A in NN/NT, B in NT): index r owns
-//    CR = KT*bytes/16 chunks; its chunk c sits at position r*CR + (c ^ swz(r)), so the
+//    CR = SK*bytes/16 chunks; its chunk c sits at position r*CR + (c ^ swz(r)), so the
 //    lanes of one read (consecutive r, same c) land in different banks.
 //  * k-major (the operand stores indices contiguously: B in NN/TN, A in TN): step s owns
 //    RC = BM*bytes/16 chunks holding the BM indices in order.
-template <int T, bool IMAJ>
+template <int T, bool IMAJ, int SK = KT>
 struct Slice {
   static constexpr int EB = Elem<T>::bytes;
   static constexpr int CE = Elem<T>::per16;
-  static constexpr int NCH = BM * KT * EB / 16;  // 1024 / 512 / 256
+  static constexpr int NCH = BM * SK * EB / 16;  // at KT: 1024 / 512 / 256
   static constexpr int NI = NCH / 64;            // load instructions per slice: 16 / 8 / 4
-  static constexpr int CR = KT * EB / 16;        // 8 / 4 / 2
+  static constexpr int CR = SK * EB / 16;        // 8 / 4 / 2
   static constexpr int RC = BM * EB / 16;        // 32 / 16 / 8
   static constexpr int PER_WAVE = (NI + NWAVES - 1) / NWAVES;
 
@@ -51,9 +51,9 @@ struct Slice {
 // 2^31); a chunk past a row's end reads the next row's bytes.  Neither reaches a stored
 // cell: indices past m or n are never stored, steps past k are never executed.  The host
 // keeps RPI * pitch * bytes below 2^30.
-template <int T, bool IMAJ>
+template <int T, bool IMAJ, int SK = KT>
 struct DirectLoader {
-  using S = Slice<T, IMAJ>;
+  using S = Slice<T, IMAJ, SK>;
   static constexpr int RPI = IMAJ ? 64 / S::CR : 64 / S::RC;  // stored rows per instruction
   uint32_t voff[S::PER_WAVE];
   __amdgpu_buffer_rsrc_t rs[S::PER_WAVE];
@@ -69,7 +69,7 @@ struct DirectLoader {
       if constexpr (IMAJ) voff[h] = (uint32_t)(((di - q * RPI) * pitch + dk) * S::EB);
       else voff[h] = (uint32_t)(((dk - q * RPI) * pitch + di) * S::EB);
     }
-    slice_step = (uint32_t)(IMAJ ? KT * S::EB : KT * pitch * S::EB);
+    slice_step = (uint32_t)(IMAJ ? SK * S::EB : SK * pitch * S::EB);
     soff = 0x7FFFFFFFu;  // the first issue builds the resources
   }
 
@@ -124,9 +124,9 @@ __device__ __forceinline__ void lds_barrier() {
 // `idx` of the slice.  bf16 widens exactly (bits << 16); int8 is f32(code) * scale, one
 // rounding, the scale flushed on input by MODE.FP_DENORM = 2 (and the product by the
 // MFMA's input flush), i.e. ftz(f32(code) * ftz(scale)).
-template <int T, bool IMAJ>
+template <int T, bool IMAJ, int SK = KT>
 __device__ __forceinline__ f4 read4(const char* slice, int idx, int s, float scale) {
-  using S = Slice<T, IMAJ>;
+  using S = Slice<T, IMAJ, SK>;
   f4 v;
   if constexpr (IMAJ) {
     const int c = s * S::EB / 16;              // chunk holding step s

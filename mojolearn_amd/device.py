@@ -164,6 +164,63 @@ def gemm_int8i32(qa, ea, qb, eb, *, out=None):
     return c
 
 
+def f16_widen(bits):
+    """float32 of float16 bits (int16/uint16/float16 tensor), exact (gemm/f16_widen.mojo:12-37)."""
+    if bits.dtype not in (torch.int16, torch.uint16, torch.float16):
+        raise TypeError("bits must hold float16 bits as int16/uint16/float16")
+    out = torch.empty(bits.shape, dtype=torch.float32, device=bits.device)
+    with torch.cuda.device(bits.device):
+        _native.check(_native.lib().mlg_f16_widen(out.data_ptr(), bits.data_ptr(), bits.numel(), _stream(bits)))
+    return out
+
+
+def int15_quantize(x):
+    """(hi int8, lo int8, exponents int32) of a float32 (rows, cols) tensor, profile int15i64.v1."""
+    _check(x, "x", torch.float32)
+    if x.dim() != 2 or x.numel() == 0:
+        raise ValueError("x must be 2-D and non-empty")
+    rows, cols = x.shape
+    hi = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    lo = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    exps = torch.empty((rows,), dtype=torch.int32, device=x.device)
+    with torch.cuda.device(x.device):
+        _native.check(_native.lib().mlg_int15_quantize(hi.data_ptr(), lo.data_ptr(), exps.data_ptr(), x.data_ptr(),
+                                                       rows, cols, _stream(x)))
+    return hi, lo, exps
+
+
+def int15_dequantize(hi, lo, exps):
+    """float32 ftz((hi * 128 + lo) * 2^exps[row])."""
+    _check(hi, "hi", torch.int8)
+    _check(lo, "lo", torch.int8)
+    _check(exps, "exponents", torch.int32)
+    if hi.dim() != 2 or hi.numel() == 0 or lo.shape != hi.shape or exps.numel() != hi.shape[0]:
+        raise ValueError("hi and lo must be 2-D, non-empty and alike, with one exponent per row")
+    rows, cols = hi.shape
+    out = torch.empty((rows, cols), dtype=torch.float32, device=hi.device)
+    with torch.cuda.device(hi.device):
+        _native.check(_native.lib().mlg_int15_dequantize(out.data_ptr(), hi.data_ptr(), lo.data_ptr(), exps.data_ptr(),
+                                                         rows, cols, _stream(hi)))
+    return out
+
+
+def gemm_int15i64(ah, al, ea, bh, bl, eb, *, out=None):
+    """C = a . b^T of fifteen-bit operands given as planes (profile int15i64.v1, OP_NT)."""
+    for t, name in ((ah, "ah"), (al, "al"), (bh, "bh"), (bl, "bl")):
+        _check(t, name, torch.int8)
+    _check(ea, "ea", torch.int32)
+    _check(eb, "eb", torch.int32)
+    m, n, k = _shape(ah, bh, OP_NT)
+    if al.shape != ah.shape or bl.shape != bh.shape or ea.numel() != m or eb.numel() != n:
+        raise ValueError("planes of one operand must agree, with one exponent per row")
+    c = _prep_out(out, m, n, ah)
+    with torch.cuda.device(ah.device):
+        _native.check(_native.lib().mlg_gemm_int15i64(c.data_ptr(), ah.data_ptr(), al.data_ptr(), ea.data_ptr(),
+                                                      bh.data_ptr(), bl.data_ptr(), eb.data_ptr(), m, n, k,
+                                                      _stream(ah)))
+    return c
+
+
 T_F32, T_BF16, T_I8 = 0, 1, 2
 
 

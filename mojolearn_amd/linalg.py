@@ -25,6 +25,10 @@ PROFILE_INT8W = "mojolearn.identical.gemm.int8w-colscale-f32.v1"
 PROFILE_INT8 = f"mojolearn.identical.gemm.int8i32.v{LOWBIT_PROFILE_VERSION}"
 #: Contract L-7: the Int32 sum of k products of codes in [-127, 127] stays exact.
 INT8_MAX_K = 131072
+INT15_PROFILE_VERSION = 1
+PROFILE_INT15 = f"mojolearn.identical.gemm.int15i64.v{INT15_PROFILE_VERSION}"
+#: Contract W-4: the shared cross-term accumulator stays exact to k = 66052; a power of two below.
+INT15_MAX_K = 65536
 
 OP_NN, OP_NT, OP_TN = 0, 1, 2
 
@@ -34,6 +38,11 @@ _LIN_OP_GEMM_BF16 = 1
 _LIN_OP_GEMM_INT8 = 2
 _LIN_OP_QUANTIZE_INT8 = 3
 _LIN_OP_DEQUANTIZE_INT8 = 4
+_LIN_OP_GEMM_INT15 = 5
+_LIN_OP_QUANTIZE_INT15 = 6
+_LIN_OP_DEQUANTIZE_INT15 = 7
+_LIN_OP_FROM_F16 = 10
+_LIN_OP_INT15_VERSION = 14
 _LIN_OP_TO_BF16 = 8
 _LIN_OP_FROM_BF16 = 9
 _LIN_OP_MODE = 11
@@ -389,6 +398,122 @@ def matmul_int8(a, b, *, out=None):
     return C
 
 
+def from_f16(bits):
+    """IEEE float16 bits (a uint16 buffer, or a float16 array read as its bits) to float32,
+    exact: a subnormal float16 becomes a normal float32, every NaN keeps its sign and payload.
+    Any shape.  python/mojolearn/_linalg_impl.py:322-326, door :552-562."""
+    require_identical()
+    v = _asarray(bits)
+    if v.dtype == np.float16:
+        v = v.view(np.uint16)
+    if v.dtype.kind not in "biuf":
+        raise TypeError(f"mojolearn: bits has buffer format '{v.dtype.str}', which is not a numeric array")
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    if v.size == 0:
+        raise ValueError("mojolearn.linalg.from_f16: bits has no elements")
+    out = np.empty(v.shape, dtype=np.float32)
+    _native.call(_LIN_OP_FROM_F16, [out.ctypes.data, v.ctypes.data], [v.size])
+    return out
+
+
+def _int15_version():
+    """`_int15_binding` (bindings/linalg_ops_lowbit_door.mojo:231-248): the loaded binary's
+    fifteen-bit profile version, which must be this module's."""
+    version = _native.call(_LIN_OP_INT15_VERSION, [], [])
+    if version != INT15_PROFILE_VERSION:
+        raise RuntimeError(f"mojolearn.linalg: the loaded extension implements fifteen-bit profile version "
+                           f"{version}, this module expects {INT15_PROFILE_VERSION} ({PROFILE_INT15})")
+
+
+def _quantize15(A):
+    """`lin_quantize_int15` (door :713-729) of an admitted operand: (hi, lo, exponents)."""
+    rows, cols = A.shape
+    hi = np.empty((rows, cols), dtype=np.int8)
+    lo = np.empty((rows, cols), dtype=np.int8)
+    exps = np.empty((rows,), dtype=np.int32)
+    _native.call(_LIN_OP_QUANTIZE_INT15, [hi.ctypes.data, lo.ctypes.data, exps.ctypes.data, A.ctypes.data],
+                 [rows, cols])
+    return hi, lo, exps
+
+
+def quantize_int15(x):
+    """Quantize a 2-D float32 matrix to fifteen-bit codes stored as two int8 planes
+    (profile ``mojolearn.identical.gemm.int15i64.v1``, contract W-1..W-3).
+
+    Per row ``e = floor(log2(absmax)) - 13``; each code is
+    ``clamp(round_half_even(x * 2**-e), -16383, 16383)`` (a NaN codes to 0), split as
+    ``hi = code >> 7`` and ``lo = code & 127`` so ``code = hi * 128 + lo``.  Returns
+    ``(hi, lo, exponents)``.  python/mojolearn/_linalg_impl.py:381-395.
+    """
+    require_identical()
+    _int15_version()
+    return _quantize15(_operand(x, "x"))
+
+
+def _int15_planes(x, name, who):
+    """`_lin_int15_planes` (door :739-749)."""
+    H = _typed(x[0], np.int8, 2, name + " hi")
+    L = _typed(x[1], np.int8, 2, name + " lo")
+    E = _typed(x[2], np.int32, 1, name + " exponents")
+    if L.shape != H.shape:
+        raise ValueError(f"mojolearn.linalg.{who}: {name} lo has shape {_shape_text(L.shape)}, "
+                         f"hi has {_shape_text(H.shape)}")
+    if E.shape[0] != H.shape[0]:
+        raise ValueError(f"mojolearn.linalg.{who}: {name} exponents has shape {_shape_text(E.shape)}, "
+                         f"want ({H.shape[0]},)")
+    return H, L, E
+
+
+def dequantize_int15(hi, lo, exponents):
+    """float32 ``(hi * 128 + lo) * 2**exponents[row]`` (contract W-6, W-7) from `quantize_int15`
+    output.  door :752-774."""
+    require_identical()
+    _int15_version()
+    H, L, E = _int15_planes((hi, lo, exponents), "operand", "dequantize_int15")
+    rows, cols = H.shape
+    out = np.empty((rows, cols), dtype=np.float32)
+    _native.call(_LIN_OP_DEQUANTIZE_INT15, [out.ctypes.data, H.ctypes.data, L.ctypes.data, E.ctypes.data],
+                 [rows, cols])
+    return out
+
+
+def _int15_operand(x, name):
+    """`_lin_int15_operand` (door :777-792): a (hi, lo, exponents) triple, or a float32 matrix
+    quantized by `quantize_int15`'s rule."""
+    if type(x) is tuple and len(x) == 3:
+        return _int15_planes(x, name, "matmul_int15")
+    if type(x) is tuple:
+        raise TypeError(f"mojolearn.linalg.matmul_int15: {name} is a tuple of {len(x)}; a fifteen-bit operand "
+                        "is (hi, lo, exponents) from quantize_int15, or a float32 matrix")
+    return _quantize15(_operand(x, name))
+
+
+def matmul_int15(a, b, *, out=None):
+    """``a @ b.T`` with fifteen-bit operands under ``mojolearn.identical.gemm.int15i64.v1`` (OP_NT).
+
+    Each of `a` (m, k) and `b` (n, k) is a float32 matrix, quantized by `quantize_int15`'s
+    rule, or a ``(hi, lo, exponents)`` triple.  The exact integer sum of the code products,
+    rounded to nearest even (W-6), scaled by ``2**(ea[i] + eb[j])``.  `k` may be at most
+    65536 (`INT15_MAX_K`); larger values raise ValueError.  python/mojolearn/_linalg_impl.py:404-417,
+    door :795-840.
+    """
+    require_identical()
+    _int15_version()
+    ah, al, ea = _int15_operand(a, "a")
+    bh, bl, eb = _int15_operand(b, "b")
+    m, k = ah.shape
+    n, kb = bh.shape
+    if k != kb:
+        raise ValueError(f"mojolearn.linalg.matmul_int15: contracted extents differ, a gives k={k} and b gives k={kb}")
+    if k > INT15_MAX_K:
+        raise ValueError(f"mojolearn.linalg.matmul_int15: k={k} is above {INT15_MAX_K}, the largest contracted "
+                         f"extent {PROFILE_INT15} accepts (contract W-4)")
+    C = _out(out, m, n, "matmul_int15")
+    _native.call(_LIN_OP_GEMM_INT15, [C.ctypes.data, ah.ctypes.data, al.ctypes.data, ea.ctypes.data,
+                                      bh.ctypes.data, bl.ctypes.data, eb.ctypes.data], [m, n, k])
+    return C
+
+
 def linear(x, w, bias, *, transpose_b=False, out=None):
     """``Y = ftz(ftz(x @ w) + ftz(bias[j]))``: the product, then the LM's nn.Linear bias
     (transformer/impl/llama/modeling_llama.mojo:3979-3989), fused into the store."""
@@ -407,6 +532,7 @@ def linear(x, w, bias, *, transpose_b=False, out=None):
 
 
 __all__ = ["matmul", "matmul_bf16", "matmul_int8", "matmul_int8w", "linear", "to_bf16", "from_bf16",
-           "quantize_int8", "dequantize_int8", "numeric_mode", "profile", "require_identical", "PROFILE",
-           "PROFILE_FAMILY", "PROFILE_VERSION", "PROFILE_BF16", "PROFILE_INT8", "PROFILE_INT8W", "INT8_MAX_K",
+           "from_f16", "quantize_int8", "dequantize_int8", "matmul_int15", "quantize_int15", "dequantize_int15",
+           "numeric_mode", "profile", "require_identical", "PROFILE", "PROFILE_FAMILY", "PROFILE_VERSION",
+           "PROFILE_BF16", "PROFILE_INT8", "PROFILE_INT15", "PROFILE_INT8W", "INT8_MAX_K", "INT15_MAX_K",
            "OP_NN", "OP_NT", "OP_TN"]

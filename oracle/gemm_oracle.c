@@ -522,6 +522,27 @@ void orc_q15_gemm(float* c, const int8_t* ah, const int8_t* al, const int32_t* e
     }
 }
 
+/* gemm/f16_widen.mojo:12-37 f16_bits_to_f32_bits: float16 bits widened exactly, a subnormal
+ * renormalized, NaN payloads kept. */
+void orc_f16_widen(uint32_t* out, const uint16_t* in, int64_t count) {
+  for (int64_t i = 0; i < count; ++i) {
+    const uint32_t h = in[i];
+    const uint32_t s = (h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x03FFu;
+    if (e == 0u) {
+      if (m == 0u) { out[i] = s; continue; }
+      uint32_t shift = 0;
+      while ((m & 0x0400u) == 0u) { m <<= 1; ++shift; }
+      m &= 0x03FFu;
+      out[i] = s | ((113u - shift) << 23) | (m << 13);
+    } else if (e == 31u) {
+      out[i] = s | 0x7F800000u | (m << 13);
+    } else {
+      out[i] = s | ((e + 112u) << 23) | (m << 13);
+    }
+  }
+}
+
 uint64_t orc_fnv1a64(const void* data, int64_t nbytes) {
   const uint8_t* p = (const uint8_t*)data;
   uint64_t h = 0xCBF29CE484222325ull;

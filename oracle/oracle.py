@@ -54,6 +54,7 @@ def lib():
         L.orc_q15_quantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_quantize_rows.restype = None
         L.orc_q15_dequantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_dequantize_rows.restype = None
         L.orc_q15_gemm.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q15_gemm.restype = None
+        L.orc_f16_widen.argtypes = [vp, vp, i64]; L.orc_f16_widen.restype = None
         L.orc_card_fill.argtypes = [vp, i64, i64]; L.orc_card_fill.restype = None
         L.orc_ftz.argtypes = [f32]; L.orc_ftz.restype = f32
         L.orc_fma.argtypes = [f32, f32, f32]; L.orc_fma.restype = f32
@@ -279,3 +280,11 @@ def q15_i64_to_f32(v):
 
 def q15_row_exponent(absmax):
     return lib().orc_q15_row_exponent(float(absmax))
+
+
+def f16_widen(bits):
+    """float16 bits (uint16) -> float32, exact, NaN payloads kept (gemm/f16_widen.mojo:12-37)."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.uint32)
+    lib().orc_f16_widen(_p(out), _p(bits), bits.size)
+    return out.view(np.float32)

@@ -64,8 +64,18 @@ def test_op_table_errors_come_through_the_sink_once():
         _native.call(0, [1, 2, 3], [1, 1, 1])
     with pytest.raises(RuntimeError, match="must all be positive"):
         _native.call(0, [1, 2, 3], [0, 1, 1, 0])
-    with pytest.raises(RuntimeError, match="not part of this build"):
-        _native.call(5, [1, 2, 3, 4, 5, 6, 7], [1, 1, 1])
+    with pytest.raises(RuntimeError, match="invalid gemm_int15 address count"):
+        _native.call(5, [1, 2, 3, 4, 5, 6], [1, 1, 1])
+    with pytest.raises(RuntimeError, match=r"gemm_int15: params must contain 3 values \(m, n, k\), got 2"):
+        _native.call(5, [1, 2, 3, 4, 5, 6, 7], [1, 1])
+    with pytest.raises(RuntimeError, match=r"gemm_int15: k must be at most 65536 \(contract W-4\), got 65537"):
+        _native.call(5, [1, 2, 3, 4, 5, 6, 7], [1, 1, 65537])
+    with pytest.raises(RuntimeError, match="quantize_int15: rows and cols must be positive, got 2 x 0"):
+        _native.call(6, [1, 2, 3, 4], [2, 0])
+    with pytest.raises(RuntimeError, match="invalid dequantize_int15 address count"):
+        _native.call(7, [1, 2, 3], [2, 2])
+    with pytest.raises(RuntimeError, match="from_f16: count must be positive, got 0"):
+        _native.call(10, [1, 2], [0])
     with pytest.raises(RuntimeError, match="invalid gemm_int8 address count"):
         _native.call(2, [1, 2, 3, 4], [1, 1, 1])
     with pytest.raises(RuntimeError, match=r"gemm_int8: params must contain 3 values \(m, n, k\), got 4"):

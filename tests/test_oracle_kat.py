@@ -365,3 +365,15 @@ def test_int15_gemm_at_max_k(oracle):
     e0 = np.zeros(1, np.int32)
     got = oracle.q15_gemm(ah, al, e0, ah, al, e0)
     assert got[0, 0] == np.array([16383 * 16383 * k], np.int64).astype(np.float32)[0]
+
+
+def test_f16_widen_all_patterns(oracle):
+    """All 65536 float16 patterns: numbers and infinities equal numpy's exact float16 ->
+    float32 conversion; every NaN keeps its sign and payload, quiet bit included as given."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_widen(bits).view(np.uint32)
+    f16 = bits.view(np.float16)
+    num = ~np.isnan(f16)
+    assert np.array_equal(got[num], f16[num].astype(np.float32).view(np.uint32))
+    b = bits[~num].astype(np.uint32)
+    assert np.array_equal(got[~num], ((b & 0x8000) << 16) | 0x7F800000 | ((b & 0x03FF) << 13))
