@@ -265,6 +265,68 @@ def bench_int8i32(torch, O, steps, warmup, check):
     return out
 
 
+#: The reference's int15i64.v1 rows on MI325X (its integer-MMA plan, best ms of its runs;
+#: bench/results/lowbit_amd_tuned/2026-09-29/mi325x/*/int15.tsv).
+INT15I64_ROWS = [("qkv.t1", 1, 4096, 4096, 0.0799), ("qkv.t8", 8, 4096, 4096, 0.0813),
+                 ("qkv.t512", 512, 4096, 4096, 0.5322), ("mlp_up.t1", 1, 14336, 4096, 0.1077),
+                 ("mlp_up.t512", 512, 14336, 4096, 1.8390), ("mlp_down.t1", 1, 4096, 14336, 0.2830),
+                 ("mlp_down.t512", 512, 4096, 14336, 1.7749), ("lm_head.t1", 1, 128256, 4096, 0.5924),
+                 ("lm_head.t512", 512, 16032, 4096, 2.0671)]
+
+
+class Int15Call:
+    """One int15i64.v1 product C = a . b^T on device planes, launched on a given stream."""
+
+    def __init__(self, torch, ah, al, ea, bh, bl, eb):
+        from mojolearn_amd import _native
+        self.lib, self.check = _native.lib(), _native.check
+        self.t = (ah, al, ea, bh, bl, eb)
+        self.m, self.k = ah.shape
+        self.n = bh.shape[0]
+        self.out = torch.empty((self.m, self.n), dtype=torch.float32, device=ah.device)
+        nb = self.lib.mlg_gemm_int15i64_workspace_bytes(ah.data_ptr(), al.data_ptr(), bh.data_ptr(), bl.data_ptr(),
+                                                        self.m, self.n, self.k)
+        if nb < 0:
+            raise RuntimeError(self.lib.mlg_last_error().decode())
+        self.nb = nb
+        self.ws = torch.empty(max(nb, 4), dtype=torch.uint8, device=ah.device)
+
+    def __call__(self, stream=None):
+        import torch
+        s = stream if stream is not None else torch.cuda.current_stream()
+        ah, al, ea, bh, bl, eb = self.t
+        self.check(self.lib.mlg_gemm_int15i64_ws(self.out.data_ptr(), ah.data_ptr(), al.data_ptr(), ea.data_ptr(),
+                                                 bh.data_ptr(), bl.data_ptr(), eb.data_ptr(), self.m, self.n, self.k,
+                                                 self.ws.data_ptr(), self.nb, s.cuda_stream))
+
+
+def bench_int15i64(torch, O, steps, warmup, check):
+    """The int15i64.v1 product (four int8 plane products per step on the integer matrix unit)
+    on the reference's Llama-8B rows, planes and exponents resident in HBM."""
+    rng = np.random.default_rng(15)
+    out = {}
+    for name, m, n, k, ref_ms in INT15I64_ROWS:
+        qa = rng.integers(-16383, 16384, (m, k))
+        qb = rng.integers(-16383, 16384, (n, k))
+        ah, al = (qa >> 7).astype(np.int8), (qa & 127).astype(np.int8)
+        bh, bl = (qb >> 7).astype(np.int8), (qb & 127).astype(np.int8)
+        del qa, qb
+        ea = rng.integers(-40, -20, m).astype(np.int32)
+        eb = rng.integers(-40, -20, n).astype(np.int32)
+        call = Int15Call(torch, *(_t(torch, x) for x in (ah, al, ea, bh, bl, eb)))
+        ms = graph_time([call], steps, warmup, torch)
+        row = {"ms": ms, "tops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "reference_mi325x_ms": ref_ms,
+               "speedup_vs_reference": ref_ms / ms}
+        if check:
+            rows = _rows(m, 4)
+            want = O.nan_canon(O.q15_gemm(ah[rows], al[rows], ea[rows], bh, bl, eb))
+            row["mismatched_words"] = _mismatch(call.out.cpu().numpy()[rows], want)
+            row["checked_cells"] = int(len(rows) * n)
+        out[name] = row
+        del call
+    return out
+
+
 def copy_calibration(torch, nbytes=1 << 30):
     """Three copies of a 1 GiB float32 buffer (torch's elementwise copy kernel): each dispatch
     reads and writes exactly `nbytes`, the yardstick for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -329,6 +391,7 @@ def main():
     if args.compare:
         extra["compare"] = bench_compare(torch, D, args.steps, args.warmup)
         extra["int8i32"] = bench_int8i32(torch, O, args.steps, args.warmup, check)
+        extra["int15i64"] = bench_int15i64(torch, O, args.steps, args.warmup, check)
 
     line = {
         "metric": "identical-mode FP32 GEMM TFLOP/s & % of peak; GEMV GB/s; 0 mismatched bits",
