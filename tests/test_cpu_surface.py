@@ -140,3 +140,60 @@ def test_workload_generators_are_deterministic():
     assert codes.dtype == np.int8 and codes.min() >= -127 and scales.min() >= 1e-3 and scales.max() <= 1e-2
     a2, _ = W.gemm512()
     assert np.array_equal(a, a2)
+
+
+def test_lowbit_containers_and_refusals():
+    """The lowbit containers and refusals that run before any conversion
+    (python/mojolearn/lowbit.py; providers/python/lowbit_weight_pyapi_door.mojo:52-170)."""
+    from mojolearn_amd import lowbit
+    bf = lowbit.BF16Weight(np.arange(24, dtype=np.uint16).reshape(6, 4))
+    q8 = lowbit.Int8Weight(np.arange(24, dtype=np.int8).reshape(6, 4), np.arange(6, dtype=np.int32) - 3)
+    assert bf.shape == (6, 4) and bf.format == "bfloat16" and q8.shape == (6, 4) and q8.format == "int8"
+    assert lowbit.is_packed(bf) and lowbit.is_packed(q8) and not lowbit.is_packed(np.ones((2, 2), np.float32))
+    assert lowbit.format_of({"w": bf, "n": np.ones(3, np.float32)}) == "bfloat16"
+    assert lowbit.format_of((q8,)) == "int8" and lowbit.format_of([]) == "float32"
+    with pytest.raises(ValueError, match="store a model one way"):
+        lowbit.format_of({"a": bf, "b": q8})
+    with pytest.raises(TypeError, match="bits must be a 2-D uint16 array"):
+        lowbit.BF16Weight(np.zeros(4, np.uint16))
+    with pytest.raises(TypeError, match="codes must be a 2-D int8 array"):
+        lowbit.Int8Weight(np.zeros((2, 2), np.uint8), np.zeros(2, np.int32))
+    with pytest.raises(TypeError, match="exponents must be int32 of shape"):
+        lowbit.Int8Weight(np.zeros((2, 2), np.int8), np.zeros(3, np.int32))
+    with pytest.raises(ValueError, match="minimum of 1 is required"):
+        lowbit.BF16Weight(np.zeros((0, 4), np.uint16))
+    a = np.ones((4, 3), np.float32)
+    with pytest.raises(ValueError, match="unknown format 'float16'"):
+        lowbit.pack_one(a, "float16")
+    with pytest.raises(ValueError, match="must be 2-D to pack, got shape \\(4,\\)"):
+        lowbit.pack_one(a[:, 0], "bfloat16")
+    with pytest.raises(TypeError, match="pack takes float32"):
+        lowbit.pack_one(a.astype(np.float64), "int8")
+    with pytest.raises(TypeError, match="must be a dict keyed by name"):
+        lowbit.pack([a], "int8")
+    with pytest.raises(TypeError, match="format must be an exact string"):
+        lowbit.pack({"a": a}, 8)
+    # float32 packing copies; non-dicts unpack as themselves; a float32 model unpacks as is
+    f = lowbit.pack_one(a, "float32")
+    assert f is not a and np.array_equal(f, a)
+    assert lowbit.unpack(a) == (a, "float32")
+    w = {"a": a}
+    assert lowbit.unpack(w) == (w, "float32")
+
+
+@pytest.mark.parametrize("fmt", ["bfloat16", "int8"])
+def test_lowbit_repack_same_format_copies_without_materializing(monkeypatch, fmt):
+    from mojolearn_amd import lowbit
+    if fmt == "bfloat16":
+        original = lowbit.BF16Weight(np.arange(24, dtype=np.uint16).reshape(6, 4))
+    else:
+        original = lowbit.Int8Weight(np.arange(24, dtype=np.int8).reshape(6, 4), np.arange(6, dtype=np.int32) - 3)
+    monkeypatch.setattr(lowbit, "materialize_one", lambda *a, **k: pytest.fail("materialized"))
+    copied = lowbit.pack({"w": original}, fmt)["w"]
+    assert copied is not original
+    if fmt == "bfloat16":
+        assert np.array_equal(copied.bits, original.bits) and not np.shares_memory(copied.bits, original.bits)
+    else:
+        assert np.array_equal(copied.codes, original.codes) and not np.shares_memory(copied.codes, original.codes)
+        assert np.array_equal(copied.exponents, original.exponents)
+        assert not np.shares_memory(copied.exponents, original.exponents)

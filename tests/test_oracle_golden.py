@@ -72,3 +72,14 @@ def test_verify_gemm_lanes(oracle, kind):
     assert VL.train_hash(lane) == cells[f"gemm-int8/{kind}"]["train"]
     lane = VL.lane_gemm_int15(S.quantize_int15, S.matmul_int15, S.dequantize_int15, oracle.INT15_MAX_K, X)
     assert VL.train_hash(lane) == cells[f"gemm-int15/{kind}"]["train"]
+
+
+@pytest.mark.parametrize("kind", VL.FIXTURES)
+def test_verify_lowbit_conversions_lane(oracle, kind, monkeypatch):
+    """The lowbit-conversions cells with the storage module's conversions answered by the oracle:
+    pins the module's object logic (predicates, refusals, ranks) and the oracle's conversions."""
+    from mojolearn_amd import lowbit
+    monkeypatch.setattr(lowbit, "_linalg", VL.OracleConversions(oracle))
+    X = VL.fixture_x(kind)
+    lane = VL.lane_lowbit_conversions(lowbit, oracle.bf16_widen, oracle, X)
+    assert VL.train_hash(lane) == VL.golden()["cells"][f"lowbit-conversions/{kind}"]["train"]

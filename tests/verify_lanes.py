@@ -3,7 +3,7 @@
 Fixtures: tools/identity_break.py:1393 (N, D = 20000, 16) and :1414-1485 (`fixture`,
 `_hashed_uniform`).  Hashes: `_h` / `_train_hash` (:1355-1382).  Lanes: gemm-pinned
 (:2984-2995), gemm-transposed (:5880-5890), gemm-bf16 (:3825-3836), gemm-int8 (:3839-3849),
-gemm-int15 (:3852-3879).  The recorded
+gemm-int15 (:3852-3879), lowbit-conversions (:4024-4234).  The recorded
 `train` hashes are in tests/golden/verify_gemm_cells.json (from
 python/mojolearn/verify_reference/table.json).
 
@@ -149,6 +149,79 @@ def lane_gemm_int15(quantize_int15, matmul_int15, dequantize_int15, int15_max_k,
     return dict(planes=h(np.asarray(ah), np.asarray(al), np.asarray(bh), np.asarray(bl)),
                 exps=h(np.asarray(ea), np.asarray(eb)), product=h(c), onecall=h(c1), flags=h(same, refuses),
                 dequant=h(np.asarray(dequantize_int15(bh, bl, eb))))
+
+
+LOWBIT_ROWS, LOWBIT_COLS = 64, 16
+
+
+def lane_lowbit_conversions(lowbit, from_bf16, O, X):
+    """The low-bit storage seams as a user reaches them (`pack_one`, `materialize_one`,
+    `widen_bf16`, `format_of`, `is_packed`, `linalg.from_bf16`) on a 64 x 16 block of the
+    fixture: the stored bytes, their float32 images, the same widening at three ranks, the
+    predicates and refusals, and agreement with an independent construction (`O`, the CPU
+    oracle, in the place of the harness's pure-Python spelling)."""
+    a2 = np.ascontiguousarray(X[:LOWBIT_ROWS, :LOWBIT_COLS]).astype(np.float32)
+    bf = lowbit.pack_one(a2, "bfloat16")
+    q8 = lowbit.pack_one(a2, "int8")
+    f32 = lowbit.pack_one(a2, "float32")
+    bits = np.asarray(bf.bits)
+    codes, exps = np.asarray(q8.codes), np.asarray(q8.exponents)
+    mbf = np.asarray(lowbit.materialize_one(bf))
+    mq8 = np.asarray(lowbit.materialize_one(q8))
+    w1 = np.asarray(lowbit.widen_bf16(bits.reshape((LOWBIT_ROWS * LOWBIT_COLS,))))
+    w3 = np.asarray(lowbit.widen_bf16(bits.reshape((4, LOWBIT_ROWS // 4, LOWBIT_COLS))))
+    lin = np.asarray(from_bf16(bits))
+    py_bits = O.bf16_narrow(a2)
+    py_wide = O.bf16_widen(bits)
+    py_codes, py_exps = O.q8_quantize(a2)
+    py_deq = O.q8_dequantize(codes, exps)
+
+    def refuses(fn, text):
+        try:
+            fn()
+        except Exception as exc:  # noqa: BLE001 -- a refusal is recorded as a number
+            return text in str(exc)
+        return False
+
+    flags = np.array([
+        lowbit.is_packed(bf), lowbit.is_packed(q8), lowbit.is_packed(a2), lowbit.is_packed(f32),
+        lowbit.format_of({"w": bf}) == "bfloat16", lowbit.format_of({"w": q8}) == "int8",
+        lowbit.format_of({"w": a2}) == "float32", lowbit.format_of([bf, a2]) == "bfloat16",
+        refuses(lambda: lowbit.format_of({"a": bf, "b": q8}), "store a model one way"),
+        bf.format == "bfloat16" and tuple(bf.shape) == (LOWBIT_ROWS, LOWBIT_COLS),
+        q8.format == "int8" and tuple(q8.shape) == (LOWBIT_ROWS, LOWBIT_COLS),
+        refuses(lambda: lowbit.pack_one(a2[:, 0], "bfloat16"), "must be 2-D to pack"),
+        refuses(lambda: lowbit.pack_one(a2, "float16"), "unknown format"),
+        lin.tobytes() == mbf.tobytes(), w1.tobytes() == mbf.tobytes(), w3.tobytes() == mbf.tobytes(),
+        np.asarray(f32).tobytes() == a2.tobytes(),
+        py_bits.tobytes() == bits.tobytes(), py_wide.tobytes() == mbf.tobytes(),
+        np.asarray(py_codes).tobytes() == codes.tobytes(), np.asarray(py_exps).tobytes() == exps.tobytes(),
+        py_deq.tobytes() == mq8.tobytes(),
+        False,
+    ], dtype=np.int64)
+    return dict(bf16_bits=h(bits), int8=h(codes, exps), materialized=h(mbf, mq8), widened=h(w1, w3),
+                f32_copy=h(np.asarray(f32)), linalg=h(lin), flags=h(flags))
+
+
+class OracleConversions:
+    """The four conversions the lowbit module calls (`to_bf16`, `from_bf16`, `quantize_int8`,
+    `dequantize_int8`), answered by the CPU oracle: installed in place of the module's linalg
+    to run the lowbit lane on a machine with no GPU."""
+
+    def __init__(self, O):
+        self.O = O
+
+    def to_bf16(self, x):
+        return self.O.bf16_narrow(np.ascontiguousarray(x, dtype=np.float32))
+
+    def from_bf16(self, bits):
+        return self.O.bf16_widen(bits)
+
+    def quantize_int8(self, x):
+        return self.O.q8_quantize(x)
+
+    def dequantize_int8(self, codes, exps):
+        return self.O.nan_canon(self.O.q8_dequantize(codes, exps))
 
 
 class OracleSurface:
