@@ -15,6 +15,17 @@ _lib = None
 SINK_T = ctypes.CFUNCTYPE(None, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64)
 
 
+def _share_hip_runtime():
+    """Load PyTorch (when installed) before the library, so that the library's HIP runtime
+    dependency binds to the one PyTorch-ROCm already carries.  A process then holds a single
+    HIP runtime; with two (the system's and PyTorch's), whichever initialises second finds no
+    GPU."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib():
     """The loaded libmlgemm.so, with argument types declared."""
     global _lib
@@ -23,6 +34,7 @@ def lib():
     with _lock:
         if _lib is not None:
             return _lib
+        _share_hip_runtime()
         if not os.path.exists(LIB_PATH):
             raise ImportError(
                 f"mojolearn_amd: {LIB_PATH} is not built; run `python -c \"import __graft_entry__ as g; g.build()\"` "

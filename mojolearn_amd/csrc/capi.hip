@@ -19,6 +19,7 @@
 #include "contract.h"
 #include "kernels.h"
 #include "q8.h"
+#include "transport.h"
 
 namespace {
 
@@ -131,8 +132,9 @@ int guarded(const std::function<void()>& fn) {
 }
 
 // ---- host-pointer transport (the role of gemm/host_entry.mojo:79-197 and
-// gemm/host_transport.mojo:107-272): pooled device buffers guarded by a busy flag; a
-// concurrent second caller gets fresh buffers.
+// gemm/host_transport.mojo:107-272): pooled device buffers guarded by a busy flag, and the
+// staged transport (transport.h) on an upload and a download stream beside the compute
+// stream.  A concurrent second caller gets fresh buffers, one stream and plain copies.
 struct DeviceBuf {
   void* ptr = nullptr;
   size_t cap = 0;
@@ -154,14 +156,33 @@ struct DeviceBuf {
   }
 };
 
+// Row bands of a host product: at most MAX_BANDS, each about BAND_BYTES of A.
+constexpr int MAX_BANDS = 8;
+constexpr size_t BAND_BYTES = size_t(16) << 20;
+
 struct HostPool {
   DeviceBuf c, a, b, x, y, w, a2, b2;
-  hipStream_t stream = nullptr;
+  hipStream_t stream = nullptr;   // products
+  mlt::Stager* stager = nullptr;  // pooled set only; never destroyed: its workers live with the process
+  hipEvent_t evc[MAX_BANDS] = {};
 };
 
 std::atomic<int> g_pool_busy{0};
 HostPool g_pool;
 std::mutex g_pool_init;
+
+void init_pooled_set(HostPool& P) {
+  if (!P.stream) hip_check(hipStreamCreateWithFlags(&P.stream, hipStreamNonBlocking), "hipStreamCreate");
+  for (hipEvent_t& e : P.evc)
+    if (!e) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+  if (!P.stager) {
+    try {
+      P.stager = new mlt::Stager();
+    } catch (const std::exception& ex) {
+      throw Fail(ex.what());
+    }
+  }
+}
 
 struct Lease {
   HostPool* pool;
@@ -171,8 +192,13 @@ struct Lease {
     int expect = 0;
     pooled = g_pool_busy.compare_exchange_strong(expect, 1);
     if (pooled) {
-      std::lock_guard<std::mutex> lock(g_pool_init);
-      if (!g_pool.stream) hip_check(hipStreamCreateWithFlags(&g_pool.stream, hipStreamNonBlocking), "hipStreamCreate");
+      try {
+        std::lock_guard<std::mutex> lock(g_pool_init);
+        init_pooled_set(g_pool);
+      } catch (...) {
+        g_pool_busy.store(0);
+        throw;
+      }
       pool = &g_pool;
     } else {
       hip_check(hipStreamCreateWithFlags(&fresh.stream, hipStreamNonBlocking), "hipStreamCreate");
@@ -197,6 +223,32 @@ void down(void* dst, const void* src, size_t bytes, hipStream_t s) {
   if (bytes) hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "hipMemcpy D2H");
 }
 
+mlt::Span span(int64_t host, void* dev, int64_t bytes, hipEvent_t after = nullptr) {
+  return mlt::Span{(void*)host, dev, (size_t)bytes, after};
+}
+
+// Uploads that the next work on P.stream reads.
+void put(HostPool& P, const std::vector<mlt::Span>& ups) {
+  if (!P.stager) {
+    for (const mlt::Span& s : ups) up(s.dev, s.host, s.bytes, P.stream);
+    return;
+  }
+  P.stager->run(ups, {});
+  P.stager->order_after_uploads(P.stream);
+}
+
+// Downloads of what the work enqueued on P.stream wrote; returns with them in host memory.
+void get(HostPool& P, std::vector<mlt::Span> downs) {
+  if (!P.stager) {
+    for (const mlt::Span& s : downs) down(s.host, s.dev, s.bytes, P.stream);
+  } else {
+    hip_check(hipEventRecord(P.evc[0], P.stream), "hipEventRecord");
+    for (mlt::Span& s : downs) s.after = P.evc[0];
+    P.stager->run({}, downs);
+  }
+  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+}
+
 std::string shape_text(int64_t m, int64_t n, int64_t k) {
   return "m=" + std::to_string(m) + " n=" + std::to_string(n) + " k=" + std::to_string(k);
 }
@@ -212,6 +264,13 @@ void refuse_host_shape(const char* who, int64_t m, int64_t n, int64_t k, int64_t
                std::to_string(op));
 }
 
+// A host product in row bands of A (OP_NN and OP_NT keep A[m][k] row-major).  Job j of the
+// staged transport uploads band j (job 0 also B, and scales or bias, and faults in the output's
+// pages) and downloads band j - 2 of C, after its product; band j is multiplied on the compute
+// stream once its upload is in.  The link carries both directions at once and the products hide
+// behind the transfers.  Every cell is computed exactly as in one launch (the leaf partition
+// depends on k only).  An output whose host memory overlaps A's takes one band, so that A is
+// read whole before any of C is written.
 int64_t host_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr, int a_type,
                   int b_type, bool with_bias) {
   const int64_t m = pr[0], n = pr[1], k = pr[2], op = pr[3];
@@ -219,23 +278,77 @@ int64_t host_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>& pr
   refuse_host_shape(who, m, n, k, op);
   Lease lease;
   HostPool& P = *lease.pool;
-  const size_t ea = a_type == mlg::T_F32 ? 4 : 2;
-  const size_t eb = b_type == mlg::T_F32 ? 4 : (b_type == mlg::T_BF16 ? 2 : 1);
-  void* dc = P.c.get((size_t)(m * n) * 4);
-  void* da = P.a.get((size_t)(m * k) * ea);
-  void* db = P.b.get((size_t)(n * k) * eb);
+  const int64_t ea = a_type == mlg::T_F32 ? 4 : 2;
+  const int64_t eb = b_type == mlg::T_F32 ? 4 : (b_type == mlg::T_BF16 ? 2 : 1);
+  char* dc = (char*)P.c.get((size_t)(m * n) * 4);
+  char* da = (char*)P.a.get((size_t)(m * k * ea));
+  void* db = P.b.get((size_t)(n * k * eb));
   float* dx = nullptr;
   if (b_type == mlg::T_I8 || with_bias) dx = (float*)P.x.get((size_t)n * 4);
-  up(da, (const void*)ad[1], (size_t)(m * k) * ea, P.stream);
-  up(db, (const void*)ad[2], (size_t)(n * k) * eb, P.stream);
-  if (dx) up(dx, (const void*)ad[3], (size_t)n * 4, P.stream);
   mlg::GemmProblem p{};
-  p.c = (float*)dc; p.a = da; p.b = db;
+  p.b = db;
   p.scales = b_type == mlg::T_I8 ? dx : nullptr;
   p.bias = with_bias ? dx : nullptr;
-  p.m = m; p.n = n; p.k = k; p.op = (int)op; p.a_type = a_type; p.b_type = b_type; p.leaf = 0;
-  enqueue_gemm(p, P.stream);
-  down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
+  p.n = n; p.k = k; p.op = (int)op; p.a_type = a_type; p.b_type = b_type; p.leaf = 0;
+
+  // bands: whole multiples of 256 rows, about BAND_BYTES of A each
+  int64_t rows = m;
+  const uintptr_t c_lo = (uintptr_t)ad[0], c_hi = c_lo + (uintptr_t)(m * n * 4);
+  const uintptr_t a_lo = (uintptr_t)ad[1], a_hi = a_lo + (uintptr_t)(m * k * ea);
+  const bool c_overlaps_a = c_lo < a_hi && a_lo < c_hi;
+  if (P.stager && op != mlg::OP_TN && !c_overlaps_a) {
+    int64_t nb = (m * k * ea) / (int64_t)BAND_BYTES;
+    nb = nb < 1 ? 1 : (nb > MAX_BANDS ? MAX_BANDS : nb);
+    rows = ((m + nb - 1) / nb + 255) / 256 * 256;
+    if (rows > m) rows = m;
+  }
+  const int64_t nb = (m + rows - 1) / rows;
+  auto band_rows = [&](int64_t j) { return (j + 1) * rows <= m ? rows : m - j * rows; };
+  auto set_band = [&](int64_t j) {
+    if (op == mlg::OP_TN) {
+      p.a = da;
+      p.c = (float*)dc;
+      p.m = m;
+    } else {
+      p.a = da + j * rows * k * ea;
+      p.c = (float*)(dc + j * rows * n * 4);
+      p.m = band_rows(j);
+    }
+  };
+  if (!P.stager) {
+    up(da, (const void*)ad[1], (size_t)(m * k * ea), P.stream);
+    up(db, (const void*)ad[2], (size_t)(n * k * eb), P.stream);
+    if (dx) up(dx, (const void*)ad[3], (size_t)n * 4, P.stream);
+    set_band(0);
+    enqueue_gemm(p, P.stream);
+    down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
+    hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+    return m * n;
+  }
+  for (int64_t j = 0; j < nb + 2; ++j) {
+    std::vector<mlt::Span> ups, downs, touch;
+    if (j == 0) {
+      ups.push_back(span(ad[2], db, n * k * eb));
+      if (dx) ups.push_back(span(ad[3], dx, n * 4));
+      touch.push_back(span(ad[0], nullptr, m * n * 4));
+    }
+    if (j < nb) {
+      if (op == mlg::OP_TN) ups.push_back(span(ad[1], da, m * k * ea));
+      else ups.push_back(span(ad[1] + j * rows * k * ea, da + j * rows * k * ea, band_rows(j) * k * ea));
+    }
+    if (j >= 2) {
+      const int64_t t = j - 2;
+      downs.push_back(op == mlg::OP_TN ? span(ad[0], dc, m * n * 4, P.evc[t])
+                                       : span(ad[0] + t * rows * n * 4, dc + t * rows * n * 4, band_rows(t) * n * 4, P.evc[t]));
+    }
+    P.stager->run(ups, downs, touch);
+    if (j < nb) {
+      P.stager->order_after_uploads(P.stream);
+      set_band(j);
+      enqueue_gemm(p, P.stream);
+      hip_check(hipEventRecord(P.evc[j], P.stream), "hipEventRecord");
+    }
+  }
   hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
   return m * n;
 }
@@ -249,10 +362,9 @@ int64_t host_from_f16(const std::vector<int64_t>& ad, const std::vector<int64_t>
   HostPool& P = *lease.pool;
   float* dout = (float*)P.c.get((size_t)count * 4);
   uint16_t* din = (uint16_t*)P.a.get((size_t)count * 2);
-  up(din, (const void*)ad[1], (size_t)count * 2, P.stream);
+  put(P, {span(ad[1], din, count * 2)});
   hip_check(mlg::run_f16_widen(dout, din, count, P.stream), "from_f16 launch");
-  down((void*)ad[0], dout, (size_t)count * 4, P.stream);
-  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  get(P, {span(ad[0], dout, count * 4)});
   return count;
 }
 
@@ -265,11 +377,10 @@ int64_t host_convert(const std::vector<int64_t>& ad, const std::vector<int64_t>&
   HostPool& P = *lease.pool;
   void* dout = P.c.get((size_t)count * (narrow ? 2 : 4));
   void* din = P.a.get((size_t)count * (narrow ? 4 : 2));
-  up(din, (const void*)ad[1], (size_t)count * (narrow ? 4 : 2), P.stream);
+  put(P, {span(ad[1], din, count * (narrow ? 4 : 2))});
   if (narrow) hip_check(mlg::run_bf16_narrow((uint16_t*)dout, (const float*)din, count, P.stream), "to_bf16 launch");
   else hip_check(mlg::run_bf16_widen((float*)dout, (const uint16_t*)din, count, P.stream), "from_bf16 launch");
-  down((void*)ad[0], dout, (size_t)count * (narrow ? 2 : 4), P.stream);
-  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  get(P, {span(ad[0], dout, count * (narrow ? 2 : 4))});
   return count;
 }
 
@@ -290,17 +401,13 @@ int64_t host_q8_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>&
   int8_t* dqb = (int8_t*)P.b.get((size_t)(n * k));
   int32_t* dea = (int32_t*)P.x.get((size_t)m * 4);
   int32_t* deb = (int32_t*)P.y.get((size_t)n * 4);
-  up(dqa, (const void*)ad[1], (size_t)(m * k), P.stream);
-  up(dea, (const void*)ad[2], (size_t)m * 4, P.stream);
-  up(dqb, (const void*)ad[3], (size_t)(n * k), P.stream);
-  up(deb, (const void*)ad[4], (size_t)n * 4, P.stream);
+  put(P, {span(ad[1], dqa, m * k), span(ad[2], dea, m * 4), span(ad[3], dqb, n * k), span(ad[4], deb, n * 4)});
   const int cus = num_cus_of_current_device();
   const int64_t wsb = mlg::q8_workspace_bytes(dqa, dqb, m, n, k, cus);
   void* dws = wsb > 0 ? P.w.get((size_t)wsb) : nullptr;
   hip_check(mlg::run_q8_gemm(dc, dqa, dea, dqb, deb, m, n, k, dws, cus, P.stream),
             "gemm_int8 launch");
-  down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
-  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  get(P, {span(ad[0], dc, m * n * 4)});
   return m * n;
 }
 
@@ -316,17 +423,14 @@ int64_t host_q8_convert(const std::vector<int64_t>& ad, const std::vector<int64_
   int8_t* dq = (int8_t*)P.a.get((size_t)(rows * cols));
   int32_t* de = (int32_t*)P.x.get((size_t)rows * 4);
   if (quantize) {  // addrs [codes, exponents, x]
-    up(df, (const void*)ad[2], (size_t)(rows * cols) * 4, P.stream);
+    put(P, {span(ad[2], df, rows * cols * 4)});
     hip_check(mlg::run_q8_quantize(dq, de, df, rows, cols, P.stream), "quantize_int8 launch");
-    down((void*)ad[0], dq, (size_t)(rows * cols), P.stream);
-    down((void*)ad[1], de, (size_t)rows * 4, P.stream);
+    get(P, {span(ad[0], dq, rows * cols), span(ad[1], de, rows * 4)});
   } else {  // addrs [y, codes, exponents]
-    up(dq, (const void*)ad[1], (size_t)(rows * cols), P.stream);
-    up(de, (const void*)ad[2], (size_t)rows * 4, P.stream);
+    put(P, {span(ad[1], dq, rows * cols), span(ad[2], de, rows * 4)});
     hip_check(mlg::run_q8_dequantize(df, dq, de, rows, cols, P.stream), "dequantize_int8 launch");
-    down((void*)ad[0], df, (size_t)(rows * cols) * 4, P.stream);
+    get(P, {span(ad[0], df, rows * cols * 4)});
   }
-  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
   return rows * cols;
 }
 
@@ -349,18 +453,13 @@ int64_t host_q15_gemm(const std::vector<int64_t>& ad, const std::vector<int64_t>
   int8_t* dbl = (int8_t*)P.b2.get((size_t)(n * k));
   int32_t* dea = (int32_t*)P.x.get((size_t)m * 4);
   int32_t* deb = (int32_t*)P.y.get((size_t)n * 4);
-  up(dah, (const void*)ad[1], (size_t)(m * k), P.stream);
-  up(dal, (const void*)ad[2], (size_t)(m * k), P.stream);
-  up(dea, (const void*)ad[3], (size_t)m * 4, P.stream);
-  up(dbh, (const void*)ad[4], (size_t)(n * k), P.stream);
-  up(dbl, (const void*)ad[5], (size_t)(n * k), P.stream);
-  up(deb, (const void*)ad[6], (size_t)n * 4, P.stream);
+  put(P, {span(ad[1], dah, m * k), span(ad[2], dal, m * k), span(ad[3], dea, m * 4), span(ad[4], dbh, n * k),
+          span(ad[5], dbl, n * k), span(ad[6], deb, n * 4)});
   const int cus = num_cus_of_current_device();
   const int64_t wsb = mlg::q15_workspace_bytes(dah, dal, dbh, dbl, m, n, k, cus);
   void* dws = wsb > 0 ? P.w.get((size_t)wsb) : nullptr;
   hip_check(mlg::run_q15_gemm(dc, dah, dal, dea, dbh, dbl, deb, m, n, k, dws, cus, P.stream), "gemm_int15 launch");
-  down((void*)ad[0], dc, (size_t)(m * n) * 4, P.stream);
-  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
+  get(P, {span(ad[0], dc, m * n * 4)});
   return m * n;
 }
 
@@ -377,19 +476,14 @@ int64_t host_q15_convert(const std::vector<int64_t>& ad, const std::vector<int64
   int8_t* dl = (int8_t*)P.a2.get((size_t)(rows * cols));
   int32_t* de = (int32_t*)P.x.get((size_t)rows * 4);
   if (quantize) {  // addrs [hi, lo, exponents, x]
-    up(df, (const void*)ad[3], (size_t)(rows * cols) * 4, P.stream);
+    put(P, {span(ad[3], df, rows * cols * 4)});
     hip_check(mlg::run_q15_quantize(dh, dl, de, df, rows, cols, P.stream), "quantize_int15 launch");
-    down((void*)ad[0], dh, (size_t)(rows * cols), P.stream);
-    down((void*)ad[1], dl, (size_t)(rows * cols), P.stream);
-    down((void*)ad[2], de, (size_t)rows * 4, P.stream);
+    get(P, {span(ad[0], dh, rows * cols), span(ad[1], dl, rows * cols), span(ad[2], de, rows * 4)});
   } else {  // addrs [y, hi, lo, exponents]
-    up(dh, (const void*)ad[1], (size_t)(rows * cols), P.stream);
-    up(dl, (const void*)ad[2], (size_t)(rows * cols), P.stream);
-    up(de, (const void*)ad[3], (size_t)rows * 4, P.stream);
+    put(P, {span(ad[1], dh, rows * cols), span(ad[2], dl, rows * cols), span(ad[3], de, rows * 4)});
     hip_check(mlg::run_q15_dequantize(df, dh, dl, de, rows, cols, P.stream), "dequantize_int15 launch");
-    down((void*)ad[0], df, (size_t)(rows * cols) * 4, P.stream);
+    get(P, {span(ad[0], df, rows * cols * 4)});
   }
-  hip_check(hipStreamSynchronize(P.stream), "hipStreamSynchronize");
   return rows * cols;
 }
 
