@@ -108,6 +108,39 @@ int mlg_gemm_ws(float* c, const void* a, const void* b, const float* scales, con
 int64_t mlg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type,
                                  int32_t b_type, int64_t leaf);
 
+/*
+ * The caller-partition and sequence-executor words on strided operand views (device pointers,
+ * enqueued on `stream`):  A_eff[i, p] = a[i a_si + p a_sp],  B_eff[p, j] = b[p b_sp + j b_sj].
+ *
+ * mlg_gemm_leaf_ptr: identical_gemm_leaf_ptr_into (gemm/neural_dispatch.mojo:245-307).  Leaf t
+ * is [t leaf, min((t + 1) leaf, k)); each leaf one ascending chain from +0, the leaves folded
+ * by the contract's tree; C dense (row stride n), not overlapping a or b.  (leaf, p_count)
+ * must partition k: (p_count - 1) leaf < k <= p_count leaf.  m or n of 0 does nothing.
+ */
+int mlg_gemm_leaf_ptr(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t leaf,
+                      int64_t p_count, int64_t a_si, int64_t a_sp, int64_t b_sp, int64_t b_sj, void* stream);
+
+/* identical_gemm_leaf_ptr_epi_into (gemm/neural_dispatch.mojo:316-397) with its follower
+ * (gemm/checks/gemm_identical.mojo:8884-8912): epi 3 PLUS_BIAS ftz(ftz(cell) + ftz(epi_p[j]));
+ * 4 BIAS_ACT ftz(act(ftz(ftz(cell) + ftz(epi_p[j])), epi_i)); 5 ACT_BWD
+ * ftz(act_bwd(ftz(cell), ftz(epi_p[i n + j]), epi_i)).  Activation codes: 0 identity,
+ * 1 logistic, 2 tanh, 3 relu, 4 softmax (left as is) (sequence/act_values.mojo:23-85).
+ * epi_p must not overlap c. */
+int mlg_gemm_leaf_ptr_epi(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t leaf,
+                          int64_t p_count, int64_t a_si, int64_t a_sp, int64_t b_sp, int64_t b_sj, int32_t epi,
+                          const float* epi_p, int32_t epi_i, void* stream);
+
+/* op_gemm (sequence/ops.mojo:518-531), the sequence executor's word: C[i ldc + j] =
+ * one ascending chain over the whole of k, started from ftz(old C[i ldc + j]) when
+ * `accumulate`, else +0.  k may be 0 (C becomes +0, or its flushed self). */
+int mlg_seq_gemm(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t a_si,
+                 int64_t a_sp, int64_t b_sp, int64_t b_sj, int64_t ldc, int32_t accumulate, void* stream);
+
+/* The followers alone over stored cells C[i ldc + j] (op_bias / op_act / op_act_bwd,
+ * sequence/ops.mojo:565-569, sequence/act_values.mojo:30-57): epi 0 flushes, 3/4/5 as above. */
+int mlg_follow(float* c, int64_t ldc, int64_t m, int64_t n, int32_t epi, const float* epi_p, int32_t epi_i,
+               void* stream);
+
 /* L-1 / L-2 conversions on device buffers (checks/numerics.mojo:1548-1574). */
 int mlg_bf16_widen(float* out, const uint16_t* in, int64_t count, void* stream);
 int mlg_bf16_narrow(uint16_t* out, const float* in, int64_t count, void* stream);

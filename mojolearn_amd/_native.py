@@ -55,6 +55,14 @@ def lib():
         L.mlg_gemm_ws.restype = ctypes.c_int
         L.mlg_gemm_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i32, i64]
         L.mlg_gemm_workspace_bytes.restype = i64
+        L.mlg_gemm_leaf_ptr.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp]
+        L.mlg_gemm_leaf_ptr.restype = ctypes.c_int
+        L.mlg_gemm_leaf_ptr_epi.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, i32, vp, i32, vp]
+        L.mlg_gemm_leaf_ptr_epi.restype = ctypes.c_int
+        L.mlg_seq_gemm.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, i32, vp]
+        L.mlg_seq_gemm.restype = ctypes.c_int
+        L.mlg_follow.argtypes = [vp, i64, i64, i64, i32, vp, i32, vp]
+        L.mlg_follow.restype = ctypes.c_int
         L.mlg_bf16_widen.argtypes = [vp, vp, i64, vp]
         L.mlg_bf16_widen.restype = ctypes.c_int
         L.mlg_bf16_narrow.argtypes = [vp, vp, i64, vp]

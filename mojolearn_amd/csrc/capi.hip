@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../../include/mlgemm.h"
+#include "act.h"
 #include "contract.h"
 #include "kernels.h"
 #include "q8.h"
@@ -607,6 +608,99 @@ int mlg_gemm_int8w(float* c, const float* a, const int8_t* codes, const float* s
     p.c = c; p.a = a; p.b = codes; p.scales = scales; p.bias = bias; p.m = m; p.n = n; p.k = k;
     p.op = op; p.a_type = mlg::T_F32; p.b_type = mlg::T_I8; p.leaf = leaf;
     enqueue_gemm(p, (hipStream_t)stream);
+  });
+}
+
+}  // extern "C"
+
+namespace {
+
+// The caller's operand views A(i, p) = a[i a_si + p a_sp], B(p, j) = b[p b_sp + j b_sj] as a
+// stored layout of the tile kernel: A row-major unless a_si == 1 != a_sp (then k-major,
+// OP_TN), B k-major unless b_sp == 1 != b_sj (then index-major, OP_NT); A and B both
+// transposed has no kernel, so A is then read as row-major (the repack gathers it).
+void view_layout(mlg::GemmProblem& p, int64_t a_si, int64_t a_sp, int64_t b_sp, int64_t b_sj) {
+  bool a_t = a_si == 1 && a_sp != 1;
+  const bool b_t = b_sp == 1 && b_sj != 1;
+  if (a_t && b_t) a_t = false;
+  p.op = a_t ? mlg::OP_TN : (b_t ? mlg::OP_NT : mlg::OP_NN);
+  p.strided = 1;
+  if (a_t) { p.a_rs = a_sp; p.a_cs = a_si; } else { p.a_rs = a_si; p.a_cs = a_sp; }
+  if (b_t) { p.b_rs = b_sj; p.b_cs = b_sp; } else { p.b_rs = b_sp; p.b_cs = b_sj; }
+  p.a_type = mlg::T_F32;
+  p.b_type = mlg::T_F32;
+  p.seq = 1;
+}
+
+void refuse_partition(const char* who, int64_t k, int64_t leaf, int64_t p_count) {
+  if (k <= 0 || leaf <= 0 || p_count <= 0 || (p_count - 1) * leaf >= k || p_count * leaf < k)
+    throw Fail(std::string(who) + ": (leaf, p_count) does not partition k");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlg_gemm_leaf_ptr(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t leaf,
+                      int64_t p_count, int64_t a_si, int64_t a_sp, int64_t b_sp, int64_t b_sj, void* stream) {
+  return guarded([&] {
+    if (m <= 0 || n <= 0) return;
+    refuse_partition("identical_gemm_leaf_ptr_into", k, leaf, p_count);
+    mlg::GemmProblem p{};
+    view_layout(p, a_si, a_sp, b_sp, b_sj);
+    p.c = c; p.a = a; p.b = b; p.m = m; p.n = n; p.k = k; p.leaf = leaf;
+    enqueue_gemm(p, (hipStream_t)stream);
+  });
+}
+
+int mlg_gemm_leaf_ptr_epi(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t leaf,
+                          int64_t p_count, int64_t a_si, int64_t a_sp, int64_t b_sp, int64_t b_sj, int32_t epi,
+                          const float* epi_p, int32_t epi_i, void* stream) {
+  return guarded([&] {
+    if (epi != mlg::EPI_PLUS_BIAS && epi != mlg::EPI_BIAS_ACT && epi != mlg::EPI_ACT_BWD)
+      throw Fail("identical_gemm_leaf_ptr_epi_into: a store epilogue kind that reads a second buffer, got " +
+                 std::to_string(epi));
+    if (m <= 0 || n <= 0) return;
+    refuse_partition("identical_gemm_leaf_ptr_epi_into", k, leaf, p_count);
+    if (!epi_p) throw Fail("identical_gemm_leaf_ptr_epi_into: the epilogue's second buffer is null");
+    mlg::GemmProblem p{};
+    view_layout(p, a_si, a_sp, b_sp, b_sj);
+    p.c = c; p.a = a; p.b = b; p.m = m; p.n = n; p.k = k; p.leaf = leaf;
+    if (epi == mlg::EPI_PLUS_BIAS) p.bias = epi_p;
+    enqueue_gemm(p, (hipStream_t)stream);
+    if (epi != mlg::EPI_PLUS_BIAS)
+      hip_check(mlg::run_follow(c, n, m, n, 0, epi, epi_p, epi_i, (hipStream_t)stream), "follower launch");
+  });
+}
+
+int mlg_seq_gemm(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t a_si,
+                 int64_t a_sp, int64_t b_sp, int64_t b_sj, int64_t ldc, int32_t accumulate, void* stream) {
+  return guarded([&] {
+    if (m < 0 || n < 0 || k < 0)
+      throw Fail("op_gemm: m, n and k must be >= 0, got " + shape_text(m, n, k));
+    if (m == 0 || n == 0) return;
+    if (m > 1 && ldc < n) throw Fail("op_gemm: the row stride of C (" + std::to_string(ldc) + ") is below n");
+    if (k == 0) {
+      hip_check(mlg::run_follow(c, ldc, m, n, accumulate ? 0 : 1, mlg::EPI_NONE, nullptr, 0, (hipStream_t)stream),
+                "follower launch");
+      return;
+    }
+    mlg::GemmProblem p{};
+    view_layout(p, a_si, a_sp, b_sp, b_sj);
+    p.c = c; p.a = a; p.b = b; p.m = m; p.n = n; p.k = k; p.leaf = k;
+    p.ldc = ldc; p.seed = accumulate ? 1 : 0;
+    enqueue_gemm(p, (hipStream_t)stream);
+  });
+}
+
+int mlg_follow(float* c, int64_t ldc, int64_t m, int64_t n, int32_t epi, const float* epi_p, int32_t epi_i,
+               void* stream) {
+  return guarded([&] {
+    if (epi != mlg::EPI_NONE && epi != mlg::EPI_PLUS_BIAS && epi != mlg::EPI_BIAS_ACT && epi != mlg::EPI_ACT_BWD)
+      throw Fail("mlg_follow: epilogue kind must be 0, 3, 4 or 5, got " + std::to_string(epi));
+    if (m <= 0 || n <= 0) return;
+    if (epi != mlg::EPI_NONE && !epi_p) throw Fail("mlg_follow: the epilogue's second buffer is null");
+    hip_check(mlg::run_follow(c, ldc, m, n, 0, epi, epi_p, epi_i, (hipStream_t)stream), "follower launch");
   });
 }
 

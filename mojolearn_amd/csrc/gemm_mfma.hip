@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
     lds_barrier(); \
   } while (0)
   static_assert(NBUF == 3, "the slice loop is unrolled by NBUF");
-  if (g.leaf % KT == 0 && ke % KT == 0) {
+  if (!g.seed && g.leaf % KT == 0 && ke % KT == 0) {
     const int spl = (int)(g.leaf / KT);
     int sl = 0;
     for (int64_t kt = kt_first; kt <= kt_last;) {
@@ -235,6 +235,18 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
       ++kt;
     }
   } else {
+    if (g.seed) {
+      // one leaf: the chain starts from the old C cell (flushed as the first step's C input)
+      const int64_t col = j0 + bcol;
+      if (col < g.n) {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+          const int blk = e >> 4, rr = e & 15;
+          const int64_t row = i0 + wr * 64 + 32 * blk + (rr & 3) + 8 * (rr >> 2) + 4 * (lane >> 5);
+          if (row < g.m) acc[e] = g.c[row * g.ldc + col];
+        }
+      }
+    }
     for (int64_t kt = kt_first; kt <= kt_last;) {
       MLG_SLICE_STEP(lds0, lds2);
       if (++kt > kt_last) break;
@@ -261,7 +273,7 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
         if (row < g.m) {
           float y = acc[e];
           if (g.bias) y = y + bj;  // ftz(C) + ftz(b) by the input flush
-          g.c[row * g.n + col] = store_word(y);
+          g.c[row * g.ldc + col] = store_word(y);
         }
       }
     } else {
@@ -280,20 +292,21 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
 // multiple of 16 bytes, zero padding), so that the product kernel's 16-byte loads are
 // aligned and never straddle a row end.
 __global__ void repack_rows_kernel(char* dst, const char* src, int64_t rows, int64_t cols, int64_t pitch,
-                                   int eb) {
+                                   int eb, int64_t s_r, int64_t s_c) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= rows * pitch) return;
   const int64_t r = i / pitch, cidx = i % pitch;
+  const int64_t from = r * s_r + cidx * s_c;
   if (eb == 4) {
-    reinterpret_cast<uint32_t*>(dst)[i] = cidx < cols ? reinterpret_cast<const uint32_t*>(src)[r * cols + cidx] : 0u;
+    reinterpret_cast<uint32_t*>(dst)[i] = cidx < cols ? reinterpret_cast<const uint32_t*>(src)[from] : 0u;
   } else if (eb == 2) {
-    reinterpret_cast<uint16_t*>(dst)[i] = cidx < cols ? reinterpret_cast<const uint16_t*>(src)[r * cols + cidx] : (uint16_t)0;
+    reinterpret_cast<uint16_t*>(dst)[i] = cidx < cols ? reinterpret_cast<const uint16_t*>(src)[from] : (uint16_t)0;
   } else {
-    dst[i] = cidx < cols ? src[r * cols + cidx] : (char)0;
+    dst[i] = cidx < cols ? src[from] : (char)0;
   }
 }
 
-__global__ void __launch_bounds__(256) fold_groups_kernel(float* c, const float* ws, const float* bias,
+__global__ void __launch_bounds__(256) fold_groups_kernel(float* c, int64_t ldc, const float* ws, const float* bias,
                                                           int64_t m, int64_t n, int64_t ngroups) {
   set_flush_inputs_mode();
   const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -306,8 +319,9 @@ __global__ void __launch_bounds__(256) fold_groups_kernel(float* c, const float*
     for (; t + 1 < ngroups; ++t) stk.push(ws[t * cells + cell], (int)t);
     y = stk.root(ws[t * cells + cell], (int)t);
   }
-  if (bias) y = y + bias[cell % n];
-  c[cell] = store_word(y);
+  const int64_t row = cell / n, col = cell - row * n;
+  if (bias) y = y + bias[col];
+  c[row * ldc + col] = store_word(y);
 }
 
 template <int OP, int AT, int BT>
@@ -334,18 +348,18 @@ hipError_t launch_mfma(const GemmArgs& g, int op, int a_type, int b_type, dim3 g
 }
 
 hipError_t launch_repack(char* dst, const char* src, int64_t rows, int64_t cols, int64_t pitch, int eb,
-                         hipStream_t stream) {
+                         int64_t s_r, int64_t s_c, hipStream_t stream) {
   const int64_t total = rows * pitch;
   hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, dst, src,
-                     rows, cols, pitch, eb);
+                     rows, cols, pitch, eb, s_r, s_c);
   return hipGetLastError();
 }
 
-hipError_t launch_fold_groups(float* c, const float* ws, const float* bias, int64_t m, int64_t n, int64_t ngroups,
-                              hipStream_t stream) {
+hipError_t launch_fold_groups(float* c, int64_t ldc, const float* ws, const float* bias, int64_t m, int64_t n,
+                              int64_t ngroups, hipStream_t stream) {
   const int64_t cells = m * n;
-  hipLaunchKernelGGL(fold_groups_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, stream, c, ws, bias,
-                     m, n, ngroups);
+  hipLaunchKernelGGL(fold_groups_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, stream, c, ldc, ws,
+                     bias, m, n, ngroups);
   return hipGetLastError();
 }
 

@@ -16,6 +16,13 @@ struct GemmProblem {
   int op;                // OP_NN, OP_NT, OP_TN
   int a_type, b_type;
   int64_t leaf;          // leaf size; 0 = the contract's (leaf_size(k))
+  // Stored-operand element strides (row, column) of A and B in the layout of `op`, read only
+  // when `strided` is set (else the operands are dense).
+  int strided;
+  int64_t a_rs, a_cs, b_rs, b_cs;
+  int64_t ldc;           // C row stride in elements; 0 = n
+  int seed;              // one leaf only: each chain starts from the flushed old C, not +0
+  int seq;               // the caller's word (strides, seed): always the tile kernel
 };
 
 // Workspace floats run_gemm needs for `p` (0 when the product folds in one launch).
@@ -35,5 +42,13 @@ hipError_t run_bf16_widen(float* out, const uint16_t* in, int64_t count, hipStre
 // IEEE float16 bits -> float32, exact (gemm/f16_widen.mojo:12-37).
 hipError_t run_f16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream);
 hipError_t run_bf16_narrow(uint16_t* out, const float* in, int64_t count, hipStream_t stream);
+
+// The product's followers over stored cells C[i * ldc + j] (i < m, j < n): `zero` first sets
+// every cell to +0 (a product over k = 0); kind 3 adds the bias p[j], kind 4 adds the bias then
+// applies activation `act`, kind 5 multiplies by the derivative of activation `act` at
+// p[i * n + j]; kind 0 stores the flushed cell.  Epilogue kinds: gemm/checks/gemm_identical.mojo
+// :8884-8912; activations sequence/act_values.mojo:60-85.
+hipError_t run_follow(float* c, int64_t ldc, int64_t m, int64_t n, int zero, int kind, const float* p, int act,
+                      hipStream_t stream);
 
 }  // namespace mlg

@@ -30,9 +30,10 @@ static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
 static int64_t gemv_groups(int64_t P) { return (P + GV_LEAVES - 1) / GV_LEAVES; }
 static int64_t gemv_cols(int bt, int op) { return op == OP_NT ? 64 : 64 * (4 / elem_bytes(bt)); }
 
-// The skinny-M path takes OP_NN products with at most GV_MAXM float32 rows.
+// The skinny-M path takes OP_NN products with at most GV_MAXM float32 rows (dense operands,
+// chains from +0).
 static bool use_gemv(const GemmProblem& p) {
-  if (p.a_type != T_F32 || p.m < 1 || p.m > GV_MAXM) return false;
+  if (p.seq || p.a_type != T_F32 || p.m < 1 || p.m > GV_MAXM) return false;
   if (p.op == OP_NN) return true;
   // OP_NT: a lane's byte offset into a 64-row block of W is 32-bit
   return p.op == OP_NT && 64 * p.k * elem_bytes(p.b_type) + 512 < (int64_t(1) << 31);
@@ -47,14 +48,35 @@ static void stored_shape(const GemmProblem& p, bool is_a, int64_t& rows, int64_t
   }
 }
 
-// Floats of workspace the MFMA path needs to repack an operand whose base is not 16-byte
-// aligned or whose rows are not a multiple of 16 bytes (0 when it is loaded in place).
+// Element strides (row, column) of a stored operand: the caller's, or dense.
+static void stored_strides(const GemmProblem& p, bool is_a, int64_t cols, int64_t& rs, int64_t& cs) {
+  rs = cols;
+  cs = 1;
+  if (p.strided) {
+    rs = is_a ? p.a_rs : p.b_rs;
+    cs = is_a ? p.a_cs : p.b_cs;
+  }
+}
+
+// Whether the MFMA path loads an operand where it lies: unit column stride, 16-byte aligned
+// base and rows, and a row stride whose 32-row span stays below the loads' offset range.
+static bool in_place(const GemmProblem& p, bool is_a) {
+  int64_t rows, cols, rs, cs;
+  stored_shape(p, is_a, rows, cols);
+  stored_strides(p, is_a, cols, rs, cs);
+  const int eb = elem_bytes(is_a ? p.a_type : p.b_type);
+  const void* base = is_a ? p.a : p.b;
+  return cs == 1 && rs > 0 && (rs * eb) % 16 == 0 && (base == nullptr || aligned(base, 16)) &&
+         (32 * rs + KT) * eb < (int64_t(1) << 30);
+}
+
+// Floats of workspace the MFMA path needs to repack an operand it cannot load in place into
+// dense rows of a multiple of 16 bytes (0 when it is loaded in place).
 static int64_t repack_floats(const GemmProblem& p, bool is_a) {
+  if (in_place(p, is_a)) return 0;
   int64_t rows, cols;
   stored_shape(p, is_a, rows, cols);
   const int eb = elem_bytes(is_a ? p.a_type : p.b_type);
-  const void* base = is_a ? p.a : p.b;
-  if ((cols * eb) % 16 == 0 && (base == nullptr || aligned(base, 16))) return 0;
   const int64_t ce = 16 / eb;
   const int64_t pitch = (cols + ce - 1) / ce * ce;
   return (rows * pitch * eb + 255) / 256 * 64;  // 256-byte granules
@@ -85,7 +107,8 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
   if (p.m <= 0 || p.n <= 0) return hipSuccess;
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
-  if (P == 0) return launch_fold_groups(p.c, nullptr, p.bias, p.m, p.n, 0, stream);
+  const int64_t ldc = p.ldc > 0 ? p.ldc : p.n;
+  if (P == 0) return launch_fold_groups(p.c, ldc, nullptr, p.bias, p.m, p.n, 0, stream);
   if (use_gemv(p)) {
     GemvArgs v;
     v.c = p.c; v.w = p.b; v.scales = p.scales; v.bias = p.bias;
@@ -114,6 +137,9 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
   GemmArgs g;
   g.c = p.c; g.a = p.a; g.b = p.b; g.scales = p.scales; g.bias = p.bias; g.ws = ws;
   g.m = p.m; g.n = p.n; g.k = p.k; g.leaf = L; g.nleaves = P;
+  g.ldc = ldc;
+  g.seed = p.seed && P == 1 ? 1 : 0;
+  if (p.seed && P != 1) return hipErrorInvalidValue;
   const int64_t tm = (p.m + BM - 1) / BM, tn = (p.n + BN - 1) / BN;
   g.tiles_n = (int)tn;
   const int64_t gsz = P > 1 ? pick_group(P, tm * tn, num_cus) : 1;
@@ -129,25 +155,29 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
     stored_shape(p, is_a, rows, cols);
     const int eb = elem_bytes(is_a ? p.a_type : p.b_type);
     const int64_t ce = 16 / eb;
-    const int64_t pitch = (cols + ce - 1) / ce * ce;
+    int64_t rs, cs;
+    stored_strides(p, is_a, cols, rs, cs);
     const void* src = is_a ? p.a : p.b;
+    int64_t pitch = rs, bytes = ((rows - 1) * rs + cols) * eb;
     if ((is_a ? ra : rb) > 0) {
-      hipError_t e = launch_repack((char*)wsp, (const char*)src, rows, cols, pitch, eb, stream);
+      pitch = (cols + ce - 1) / ce * ce;
+      bytes = rows * pitch * eb;
+      // one load instruction spans at most 32 stored rows (int8, index-major), and a slice
+      // advances a k-major operand by KT rows: both below 2^30 bytes keep the loads' lane and
+      // scalar offsets below 2^31
+      if ((32 * pitch + KT) * eb >= (int64_t(1) << 30)) return hipErrorInvalidValue;
+      hipError_t e = launch_repack((char*)wsp, (const char*)src, rows, cols, pitch, eb, rs, cs, stream);
       if (e != hipSuccess) return e;
       src = wsp;
       wsp += is_a ? ra : rb;
     }
-    if (is_a) { g.a = src; g.a_pitch = pitch; g.a_bytes = rows * pitch * eb; }
-    else { g.b = src; g.b_pitch = pitch; g.b_bytes = rows * pitch * eb; }
-    // one load instruction spans at most 32 stored rows (int8, index-major), and a slice
-    // advances a k-major operand by KT rows: both below 2^30 bytes keep the loads' lane and
-    // scalar offsets below 2^31
-    if ((32 * pitch + KT) * eb >= (int64_t(1) << 30)) return hipErrorInvalidValue;
+    if (is_a) { g.a = src; g.a_pitch = pitch; g.a_bytes = bytes; }
+    else { g.b = src; g.b_pitch = pitch; g.b_bytes = bytes; }
   }
   dim3 grid((unsigned)(tm * tn), (unsigned)g.ngroups);
   hipError_t e = launch_mfma(g, p.op, p.a_type, p.b_type, grid, stream);
   if (e != hipSuccess || g.ngroups == 1) return e;
-  return launch_fold_groups(p.c, ws, p.bias, p.m, p.n, g.ngroups, stream);
+  return launch_fold_groups(p.c, ldc, ws, p.bias, p.m, p.n, g.ngroups, stream);
 }
 
 // ---------------------------------------------------------------------------

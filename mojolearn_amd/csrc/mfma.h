@@ -36,17 +36,20 @@ struct GemmArgs {
   int64_t a_pitch, b_pitch;  // stored row lengths in elements
   int64_t a_bytes, b_bytes;  // stored operand sizes
   int tiles_n;
+  int64_t ldc;        // C row stride
+  int seed;           // one leaf: the chain starts from the old C cell
 };
 
 // Launch gemm_mfma_kernel<op, a_type, b_type> on `grid` (tiles, leaf groups).
 hipError_t launch_mfma(const GemmArgs& g, int op, int a_type, int b_type, dim3 grid, hipStream_t stream);
 
-// Copy [rows][cols] elements of `eb` bytes into [rows][pitch], zero padding.
+// Copy [rows][cols] elements of `eb` bytes, element (r, c) at src[r * s_r + c * s_c], into
+// [rows][pitch], zero padding.
 hipError_t launch_repack(char* dst, const char* src, int64_t rows, int64_t cols, int64_t pitch, int eb,
-                         hipStream_t stream);
+                         int64_t s_r, int64_t s_c, hipStream_t stream);
 
 // Fold `ngroups` group roots ws[g][m][n] per cell (0 groups: store +0.0), add bias, store.
-hipError_t launch_fold_groups(float* c, const float* ws, const float* bias, int64_t m, int64_t n, int64_t ngroups,
+hipError_t launch_fold_groups(float* c, int64_t ldc, const float* ws, const float* bias, int64_t m, int64_t n, int64_t ngroups,
                               hipStream_t stream);
 
 }  // namespace mlg

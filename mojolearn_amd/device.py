@@ -265,3 +265,84 @@ class Plan:
         if rc:
             _native.check(rc)
         return self.out
+
+
+# ---- caller-partition and sequence-executor words on strided views
+
+EPI_NONE, EPI_PLUS_BIAS, EPI_BIAS_ACT, EPI_ACT_BWD = 0, 3, 4, 5
+ACT_IDENTITY, ACT_LOGISTIC, ACT_TANH, ACT_RELU, ACT_SOFTMAX = 0, 1, 2, 3, 4
+
+
+def _view(t, name):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a device tensor")
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} has dtype {t.dtype}, want torch.float32")
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    return t.stride()
+
+
+def _views(a, b):
+    a_si, a_sp = _view(a, "a")
+    b_sp, b_sj = _view(b, "b")
+    (m, k), (kb, n) = a.shape, b.shape
+    if k != kb:
+        raise ValueError(f"contracted extents differ: a gives k={k}, b gives k={kb}")
+    return m, n, k, a_si, a_sp, b_sp, b_sj
+
+
+def _epi_buffer(epi, epi_p, m, n):
+    if epi == EPI_NONE:
+        return None
+    _check(epi_p, "epi_p", torch.float32)
+    need = m * n if epi == EPI_ACT_BWD else n
+    if epi_p.numel() != need:
+        raise ValueError(f"epi_p must hold {need} values for epilogue kind {epi}")
+    return epi_p.data_ptr()
+
+
+def gemm_leaf_ptr(a, b, *, leaf, p_count, out=None, epi=EPI_NONE, epi_p=None, act=ACT_IDENTITY):
+    """identical_gemm_leaf_ptr_into / _epi_into (gemm/neural_dispatch.mojo:245-397): C = A_eff . B_eff
+    with the caller's partition (leaf, p_count) of k, `a` an (m, k) and `b` a (k, n) view of any
+    strides; optional follower `epi` (3 bias, 4 bias + activation `act`, 5 activation derivative
+    at `epi_p`, dense (m, n))."""
+    m, n, k, a_si, a_sp, b_sp, b_sj = _views(a, b)
+    c = _prep_out(out, m, n, a)
+    p = _epi_buffer(epi, epi_p, m, n)
+    L = _native.lib()
+    with torch.cuda.device(a.device):
+        if epi == EPI_NONE:
+            rc = L.mlg_gemm_leaf_ptr(c.data_ptr(), a.data_ptr(), b.data_ptr(), m, n, k, leaf, p_count,
+                                     a_si, a_sp, b_sp, b_sj, _stream(a))
+        else:
+            rc = L.mlg_gemm_leaf_ptr_epi(c.data_ptr(), a.data_ptr(), b.data_ptr(), m, n, k, leaf, p_count,
+                                         a_si, a_sp, b_sp, b_sj, epi, p, act, _stream(a))
+        _native.check(rc)
+    return c
+
+
+def seq_gemm(a, b, c, *, accumulate=False):
+    """op_gemm (sequence/ops.mojo:518-531) in place on `c`, an (m, n) view with unit column
+    stride: one ascending chain over the whole of k per cell, from ftz(old C) when
+    `accumulate`, else +0."""
+    m, n, k, a_si, a_sp, b_sp, b_sj = _views(a, b)
+    ldc, c_sj = _view(c, "c")
+    if tuple(c.shape) != (m, n) or (c_sj != 1 and n > 1):
+        raise ValueError(f"c must be an ({m}, {n}) view with unit column stride")
+    with torch.cuda.device(a.device):
+        _native.check(_native.lib().mlg_seq_gemm(c.data_ptr(), a.data_ptr(), b.data_ptr(), m, n, k, a_si, a_sp,
+                                                 b_sp, b_sj, ldc, 1 if accumulate else 0, _stream(a)))
+    return c
+
+
+def follow(c, epi, epi_p=None, act=ACT_IDENTITY):
+    """The followers alone over the cells of `c` (an (m, n) view, unit column stride)."""
+    ldc, c_sj = _view(c, "c")
+    m, n = c.shape
+    if c_sj != 1 and n > 1:
+        raise ValueError("c must have unit column stride")
+    p = _epi_buffer(epi, epi_p, m, n)
+    with torch.cuda.device(c.device):
+        _native.check(_native.lib().mlg_follow(c.data_ptr(), ldc, m, n, epi, p, act, _stream(c)))
+    return c

@@ -566,3 +566,122 @@ void orc_card_fill(float* out, int64_t count, int64_t salt) {
 }
 
 int orc_max_threads(void) { return omp_get_max_threads(); }
+
+/* ---- the sequence executor's GEMM word and its followers ------------------------------------
+ * sequence/ops.mojo:518-531 op_gemm: C[i, j] (row stride ldc) = (accumulate ? ld(C[i, j]) : 0)
+ * then, p ascending over the whole of k, acc = fma3(ld(A(i, p)), ld(B(p, j)), acc), stored
+ * through st: acc = ftz(fma(ftz a, ftz b, acc)), one chain per cell seeded by the flushed old C
+ * (or +0).  A(i, p) = a[i a_si + p a_sp], B(p, j) = b[p b_sp + j b_sj]
+ * (sequence/ops.mojo:369-392 ld/st/mul/add/sub/fma3; gemm/neural_dispatch.mojo:245-274). */
+void orc_seq_gemm(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t a_si,
+                  int64_t a_sp, int64_t b_sp, int64_t b_sj, int64_t ldc, int accumulate) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      float acc = accumulate ? ftz(c[i * ldc + j]) : 0.0f;
+      for (int64_t p = 0; p < k; ++p) acc = ftz(fmaf(ftz(a[i * a_si + p * a_sp]), ftz(b[p * b_sp + j * b_sj]), acc));
+      c[i * ldc + j] = ftz(acc);
+    }
+}
+
+/* checks/numerics.mojo:370-408 portable_expf: Cephes single-precision expf (cephes/single/expf.c)
+ * with the reduction's multiply-add and the scaling written out as single roundings. */
+float orc_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.722835f) return u2f(0x7F800000u);
+  if (x < -87.33655f) return 0.0f;
+  const float zf = floorf(fmaf(x, 1.4426950408889634f, 0.5f));
+  const int32_t kq = (int32_t)zf;
+  float r = fmaf(zf, -0.693359375f, x);
+  r = fmaf(zf, 2.12194440e-4f, r);
+  float q = 1.9875691500e-4f;
+  q = fmaf(q, r, 1.3981999507e-3f);
+  q = fmaf(q, r, 8.3334519073e-3f);
+  q = fmaf(q, r, 4.1665795894e-2f);
+  q = fmaf(q, r, 1.6666665459e-1f);
+  q = fmaf(q, r, 5.0000001201e-1f);
+  const float r2 = r * r;
+  float y = fmaf(q, r2, r) + 1.0f;
+  const int32_t k1 = kq >> 1, k2 = kq - k1;
+  y = y * u2f((uint32_t)(k1 + 127) << 23);
+  y = y * u2f((uint32_t)(k2 + 127) << 23);
+  if (y < 1.1754943508222875e-38f) return 0.0f;
+  return y;
+}
+
+/* checks/numerics.mojo:1025-1037: flushed operands, one correctly rounded division, flushed result */
+float orc_divf(float a, float b) { return ftz(ftz(a) / ftz(b)); }
+
+/* checks/numerics.mojo:1079-1085 portable_sigmoidf: 1 / (1 + expf(-x)) */
+float orc_sigmoidf(float x) {
+  if (x != x) return x;
+  return orc_divf(1.0f, orc_expf(-x) + 1.0f);
+}
+
+/* checks/numerics.mojo:1190-1222 portable_tanhf: Cephes single-precision tanhf with the input
+ * flushed and the sign of zero kept; saturation above 0x42317218 */
+float orc_tanhf(float x_in) {
+  const float xx = ftz(x_in);
+  if (xx != xx) return xx;
+  if (xx == 0.0f) return xx;
+  const float x = fabsf(xx);
+  if (x > u2f(0x42317218u)) return xx < 0.0f ? -1.0f : 1.0f;
+  if (x >= 0.625f) {
+    const float e = orc_expf(x + x);
+    const float q = orc_divf(2.0f, e + 1.0f);
+    const float z = 1.0f - q;
+    return xx < 0.0f ? -z : z;
+  }
+  const float zs = x * x;
+  float p = -5.70498872745e-3f;
+  p = fmaf(p, zs, 2.06390887954e-2f);
+  p = fmaf(p, zs, -5.37397155531e-2f);
+  p = fmaf(p, zs, 1.33314422036e-1f);
+  p = fmaf(p, zs, -3.33332819422e-1f);
+  const float pz = p * zs;
+  return fmaf(pz, xx, xx);
+}
+
+/* sequence/act_values.mojo:60-85 act_value / act_bwd_value; codes: 0 identity, 1 logistic,
+ * 2 tanh, 3 relu, 4 softmax (no branch: the word is left) */
+float orc_act_value(float z, int code) {
+  if (code == 1) return ftz(orc_sigmoidf(z));
+  if (code == 2) return ftz(orc_tanhf(z));
+  if (code == 3) return z > 0.0f ? z : 0.0f;
+  return z;
+}
+
+float orc_act_bwd_value(float d, float z, int code) {
+  if (code == 1) return ftz(ftz(ftz(d * z) * ftz(1.0f - z)));
+  if (code == 2) return ftz(d * ftz(1.0f - ftz(z * z)));
+  if (code == 3 && z == 0.0f) return 0.0f;
+  return d;
+}
+
+/* The product's followers over its stored cells (gemm/checks/gemm_identical.mojo:8891-8912):
+ * kind 3 PLUS_BIAS  ftz(ftz(cell) + ftz(p[j]))
+ * kind 4 BIAS_ACT   ftz(act_value(ftz(ftz(cell) + ftz(p[j])), act))
+ * kind 5 ACT_BWD    ftz(act_bwd_value(ftz(cell), ftz(p[i n + j]), act))   (p dense, row stride n)
+ * c has row stride ldc. */
+void orc_epilogue(float* c, int64_t ldc, int64_t m, int64_t n, int kind, const float* p, int act) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) {
+      const float cell = ftz(c[i * ldc + j]);
+      float y = cell;
+      if (kind == 3) y = ftz(cell + ftz(p[j]));
+      else if (kind == 4) y = ftz(orc_act_value(ftz(cell + ftz(p[j])), act));
+      else if (kind == 5) y = ftz(orc_act_bwd_value(cell, ftz(p[i * n + j]), act));
+      c[i * ldc + j] = y;
+    }
+}
+
+/* elementwise maps of the functions above, for the tests: which = 0 expf, 1 sigmoidf, 2 tanhf,
+ * 3 divf(1, x) */
+void orc_map(float* out, const float* in, int64_t count, int which) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < count; ++i) {
+    const float x = in[i];
+    out[i] = which == 0 ? orc_expf(x) : which == 1 ? orc_sigmoidf(x) : which == 2 ? orc_tanhf(x) : orc_divf(1.0f, x);
+  }
+}

@@ -59,6 +59,15 @@ def lib():
         L.orc_ftz.argtypes = [f32]; L.orc_ftz.restype = f32
         L.orc_fma.argtypes = [f32, f32, f32]; L.orc_fma.restype = f32
         L.orc_max_threads.argtypes = []; L.orc_max_threads.restype = c_int
+        L.orc_seq_gemm.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, c_int]
+        L.orc_seq_gemm.restype = None
+        L.orc_epilogue.argtypes = [vp, i64, i64, i64, c_int, vp, c_int]; L.orc_epilogue.restype = None
+        L.orc_map.argtypes = [vp, vp, i64, c_int]; L.orc_map.restype = None
+        for name in ("orc_expf", "orc_sigmoidf", "orc_tanhf"):
+            getattr(L, name).argtypes = [f32]
+            getattr(L, name).restype = f32
+        L.orc_act_value.argtypes = [f32, c_int]; L.orc_act_value.restype = f32
+        L.orc_act_bwd_value.argtypes = [f32, f32, c_int]; L.orc_act_bwd_value.restype = f32
         _lib = L
     return _lib
 
@@ -288,3 +297,52 @@ def f16_widen(bits):
     out = np.empty(bits.shape, np.uint32)
     lib().orc_f16_widen(_p(out), _p(bits), bits.size)
     return out.view(np.float32)
+
+
+# ---- the sequence executor's GEMM word and its followers
+
+EPI_NONE, EPI_PLUS_BIAS, EPI_BIAS_ACT, EPI_ACT_BWD = 0, 3, 4, 5
+ACT_IDENTITY, ACT_LOGISTIC, ACT_TANH, ACT_RELU, ACT_SOFTMAX = 0, 1, 2, 3, 4
+
+
+def seq_gemm(c, a, b, m, n, k, a_si, a_sp, b_sp, b_sj, ldc, accumulate):
+    """sequence/ops.mojo:518-531 `op_gemm` on flat float32 buffers, in place on `c`: one whole-k
+    chain per cell, seeded by the flushed old C when `accumulate`, else +0."""
+    for x in (c, a, b):
+        assert x.dtype == np.float32 and x.flags.c_contiguous
+    assert c.flags.writeable
+    if m > 0 and n > 0:
+        assert c.size >= (m - 1) * ldc + n
+        assert k == 0 or a.size > (m - 1) * a_si + (k - 1) * a_sp
+        assert k == 0 or b.size > (k - 1) * b_sp + (n - 1) * b_sj
+    lib().orc_seq_gemm(_p(c), _p(a), _p(b), m, n, k, a_si, a_sp, b_sp, b_sj, ldc, 1 if accumulate else 0)
+    return c
+
+
+def epilogue(c, ldc, m, n, kind, p=None, act=0):
+    """The product's followers (gemm/checks/gemm_identical.mojo:8891-8912) in place on `c`."""
+    assert c.dtype == np.float32 and c.flags.c_contiguous
+    if kind in (EPI_PLUS_BIAS, EPI_BIAS_ACT):
+        p = _f32c(p); assert p.size >= n
+    elif kind == EPI_ACT_BWD:
+        p = _f32c(p); assert p.size >= m * n
+    else:
+        p = np.zeros(1, np.float32)
+    lib().orc_epilogue(_p(c), ldc, m, n, kind, _p(p), act)
+    return c
+
+
+def fmap(x, which):
+    """Elementwise expf (0), sigmoidf (1), tanhf (2) or 1/x (3) of the restatements."""
+    x = _f32c(x)
+    out = np.empty_like(x)
+    lib().orc_map(_p(out), _p(x), x.size, which)
+    return out
+
+
+def act_value(z, code):
+    return lib().orc_act_value(z, code)
+
+
+def act_bwd_value(d, z, code):
+    return lib().orc_act_bwd_value(d, z, code)
