@@ -45,8 +45,12 @@ struct GemvArgs {
 };
 
 // OP_NN with whole 128-row leaves and at least this many rows of X: the chains on the matrix
-// cores (gemv_mfma.hip; X 16-byte aligned, 16 * K * 4 < 2^31).
+// cores (gemv_mfma.hip; X 16-byte aligned, 16 * K * 4 < 2^31).  Its workgroups are twice as
+// wide: MF_LEAVES leaves (an aligned subtree of 8) per workgroup, so the cross-workgroup fold
+// has half the roots.
 constexpr int GV_MFMA_MIN_M = 5;
+constexpr int MF_THREADS = 512;
+constexpr int MF_LEAVES = MF_THREADS / 64;
 
 // vec (OP_NN): 0 element loads, 1 word (buffer) loads, 2 word loads of whole 128-row leaves.
 hipError_t launch_gemv_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,

@@ -154,19 +154,28 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], 
   constexpr int CPL = GvCols<BT>::cpl;
   constexpr int NBLK = GV_CH / GV_RB;
   constexpr int RING = GV_AHEAD + 1;
-  constexpr int XB = MR <= 2 ? 16 : 32 / MR;
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
+  constexpr int XB = MR <= 16 ? 16 / MR : 1;  // 16 x values a batch: two batches fit the scalar file
+  // Each block of GV_RB rows gets a resource based at its first row, so the scalar offsets
+  // are the GV_RB values i * rowbytes shared by every block (not GV_CH values held at once).
+  auto block_rs = [&](int b) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf) + (int64_t)b * GV_RB * rowbytes, (short)0,
+                                             0x7FFFFFFF, RSRC_WORD3);
+  };
   const float* xr[MR];
 #pragma unroll
   for (int r = 0; r < MR; ++r) xr[r] = xl + (r < m ? r : m - 1) * k;  // rows past m: never stored
 
   uint32_t ring[RING][GV_RB];
 #pragma unroll
-  for (int b = 0; b < GV_AHEAD; ++b)
+  for (int b = 0; b < GV_AHEAD; ++b) {
+    const __amdgpu_buffer_rsrc_t rs = block_rs(b);
+    int rb = rowbytes;
+    // With more than one row of x the offsets are recomputed per block, never held across
+    // blocks (held, they overflow the scalar file next to x).
+    if constexpr (MR > 1) __asm__ volatile("" : "+s"(rb));
 #pragma unroll
-    for (int i = 0; i < GV_RB; ++i)
-      ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * GV_RB + i) * rowbytes, 0);
+    for (int i = 0; i < GV_RB; ++i) ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, i * rb, 0);
+  }
   float xc[MR][XB], xn[MR][XB];
 #pragma unroll
   for (int r = 0; r < MR; ++r)
@@ -177,10 +186,12 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], 
   for (int b = 0; b < NBLK; ++b) {
     if (b + GV_AHEAD < NBLK) {
       __builtin_amdgcn_sched_barrier(0);
+      const __amdgpu_buffer_rsrc_t rs = block_rs(b + GV_AHEAD);
+      int rb = rowbytes;
+      if constexpr (MR > 1) __asm__ volatile("" : "+s"(rb));
 #pragma unroll
       for (int i = 0; i < GV_RB; ++i)
-        ring[(b + GV_AHEAD) % RING][i] =
-            __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ((b + GV_AHEAD) * GV_RB + i) * rowbytes, 0);
+        ring[(b + GV_AHEAD) % RING][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, i * rb, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -294,38 +305,64 @@ __device__ __forceinline__ void gv_leaf_nt(float (&acc)[MR][1], const char* w, i
 // part[wave][row][col]: the workgroup's root (the tree over its up to GV_LEAVES leaves),
 // then either the store (one group) or the count and, in the workgroup that completes it,
 // the fold of every group's root (the rest of the contract's tree), bias and store.
-template <int MR, int COLS>
-__device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[GV_LEAVES][MR][COLS],
+template <int MR, int COLS, int LEAVES = GV_LEAVES, int THREADS = GV_THREADS>
+__device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[LEAVES][MR][COLS],
                                           unsigned int& last_flag, int tid, int64_t grp, int64_t cg, int m) {
+  static_assert(LEAVES == 4 || LEAVES == 8, "a workgroup folds 4 or 8 leaves");
   __syncthreads();
-  const int64_t left = g.nleaves - grp * GV_LEAVES;
-  const int cnt = left < GV_LEAVES ? (int)left : GV_LEAVES;
-  constexpr int CPT = (MR * COLS + GV_THREADS - 1) / GV_THREADS;  // cells per thread
-  constexpr int LB = CPT < 4 ? CPT : 4;                            // cells per batch of LDS reads
-  // this thread's cells tid + c * GV_THREADS of rows < m, LB at a time: every partial of a
+  const int64_t left = g.nleaves - grp * LEAVES;
+  const int cnt = left < LEAVES ? (int)left : LEAVES;
+  constexpr int CPT = (MR * COLS + THREADS - 1) / THREADS;  // cells per thread
+  constexpr int LB = CPT < 4 ? CPT : 4;                      // cells per batch of LDS reads
+  // this thread's cells tid + c * THREADS of rows < m, LB at a time: every partial of a
   // batch read before any add
 #pragma unroll
   for (int c0 = 0; c0 < CPT; c0 += LB) {
-    float p[GV_LEAVES][LB];
+    float p[LEAVES][LB];
 #pragma unroll
     for (int c = 0; c < LB; ++c) {
-      const int cell = tid + (c0 + c) * GV_THREADS;
+      const int cell = tid + (c0 + c) * THREADS;
       const int r = cell / COLS, col = cell % COLS;
       if (c0 + c >= CPT || cell >= MR * COLS || r >= m) continue;
 #pragma unroll
-      for (int l = 0; l < GV_LEAVES; ++l)
+      for (int l = 0; l < LEAVES; ++l)
         if (l < cnt) p[l][c] = part[l][r][col];
     }
 #pragma unroll
     for (int c = 0; c < LB; ++c) {
-      const int cell = tid + (c0 + c) * GV_THREADS;
+      const int cell = tid + (c0 + c) * THREADS;
       const int r = cell / COLS, col = cell % COLS;
       const int64_t j = cg * COLS + col;
       if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
-      float y = p[0][c];
-      if (cnt >= 2) y = y + p[1][c];           // leaves 0,1 paired
-      if (cnt == 3) y = y + p[2][c];           // leaf 2 carried, then joined
-      if (cnt == 4) y = y + (p[2][c] + p[3][c]);
+      float y;
+      if (cnt == LEAVES) {
+        // the complete aligned subtree: adjacent pairs, level by level
+        float v[LEAVES];
+#pragma unroll
+        for (int l = 0; l < LEAVES; ++l) v[l] = p[l][c];
+#pragma unroll
+        for (int w = LEAVES; w > 1; w /= 2)
+#pragma unroll
+          for (int q = 0; q < w / 2; ++q) v[q] = v[2 * q] + v[2 * q + 1];
+        y = v[0];
+      } else {
+        // the tail of the tree (the last group, fewer leaves): the odd one carried up
+        float v[LEAVES];
+#pragma unroll
+        for (int l = 0; l < LEAVES; ++l) v[l] = l < cnt ? p[l][c] : 0.f;
+        int w = cnt;
+#pragma unroll 1
+        while (w > 1) {
+#pragma unroll
+          for (int q = 0; q < LEAVES / 2; ++q)
+            if (q < w / 2) v[q] = v[2 * q] + v[2 * q + 1];
+#pragma unroll
+          for (int q = 0; q < LEAVES / 2; ++q)
+            if ((w & 1) && q == w / 2) v[q] = v[w - 1];
+          w = (w + 1) / 2;
+        }
+        y = v[0];
+      }
       if (g.ngroups == 1) {
         if (g.bias) y = y + g.bias[j];  // ftz(C) + ftz(b) by the input flush
         g.c[r * g.n + j] = store_word(y);
@@ -355,7 +392,7 @@ __device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[GV_LE
       float v[CB][GV_FEW_GROUPS];
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
-        const int cell = tid + (c0 + c) * GV_THREADS;
+        const int cell = tid + (c0 + c) * THREADS;
         const int r = cell / COLS, col = cell % COLS;
         const int64_t j = cg * COLS + col;
         if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
@@ -366,7 +403,7 @@ __device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[GV_LE
       }
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
-        const int cell = tid + (c0 + c) * GV_THREADS;
+        const int cell = tid + (c0 + c) * THREADS;
         const int r = cell / COLS, col = cell % COLS;
         const int64_t j = cg * COLS + col;
         if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
@@ -386,7 +423,7 @@ __device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[GV_LE
     }
   } else {
 #pragma unroll 1
-    for (int cell = tid; cell < MR * COLS; cell += GV_THREADS) {
+    for (int cell = tid; cell < MR * COLS; cell += THREADS) {
       const int r = cell / COLS, col = cell % COLS;
       const int64_t j = cg * COLS + col;
       if (r >= m || j >= g.n) continue;

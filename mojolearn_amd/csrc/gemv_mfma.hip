@@ -22,7 +22,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // (lgkmcnt) and never makes the loop wait behind the ring's loads (vmcnt is in order).
 constexpr int GV_XS = 16 * GV_CH;  // floats of one wave's x block
 constexpr int MF_RB = 16;          // W rows per ring block
-constexpr int MF_AHEAD = 7;        // blocks requested ahead: the whole leaf in flight
+constexpr int MF_AHEAD = 3;        // blocks requested ahead of the one being consumed
 
 template <int BT>
 __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
@@ -87,7 +87,7 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
 }
 
 template <int BT>
-__global__ void __launch_bounds__(GV_THREADS) gemv_mfma_nn_kernel(GemvArgs g, const float* __restrict__ x) {
+__global__ void __launch_bounds__(MF_THREADS) gemv_mfma_nn_kernel(GemvArgs g, const float* __restrict__ x) {
   constexpr int MR = GV_MAXM;
   constexpr int CPL = GvCols<BT>::cpl;
   constexpr int COLS = GvCols<BT>::cols;
@@ -96,8 +96,8 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_mfma_nn_kernel(GemvArgs g, co
   // its leaf when that area is large enough (int8, bf16), else in an area of its own (f32).
   constexpr int PART = MR * COLS;
   constexpr int XOWN = PART >= GV_XS ? 0 : GV_XS;
-  __shared__ __attribute__((aligned(16))) float part[GV_LEAVES][MR][COLS];
-  __shared__ __attribute__((aligned(16))) float xown[GV_LEAVES][XOWN > 0 ? XOWN : 1];
+  __shared__ __attribute__((aligned(16))) float part[MF_LEAVES][MR][COLS];
+  __shared__ __attribute__((aligned(16))) float xown[MF_LEAVES][XOWN > 0 ? XOWN : 1];
   __shared__ unsigned int last_flag;
 
   set_flush_inputs_mode();
@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_mfma_nn_kernel(GemvArgs g, co
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t cg = blockIdx.x % g.ncg;
   const int64_t grp = blockIdx.x / g.ncg;
-  const int64_t t = grp * GV_LEAVES + wave;  // this wave's leaf
+  const int64_t t = grp * MF_LEAVES + wave;  // this wave's leaf
   const int m = (int)g.m;
 
   v16f acc[CPL];
@@ -139,13 +139,13 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_mfma_nn_kernel(GemvArgs g, co
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         part[wave][4 * (lane >> 4) + i][CPL * (16 * blk + (lane & 15)) + e] = acc[e][4 * blk + i];
-  gv_finish<MR, COLS>(g, part, last_flag, tid, grp, cg, m);
+  gv_finish<MR, COLS, MF_LEAVES, MF_THREADS>(g, part, last_flag, tid, grp, cg, m);
 }
 
 hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, dim3 grid, hipStream_t stream) {
-  if (b_type == T_F32) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_F32>, grid, dim3(GV_THREADS), 0, stream, g, x);
-  else if (b_type == T_BF16) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_BF16>, grid, dim3(GV_THREADS), 0, stream, g, x);
-  else hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_I8>, grid, dim3(GV_THREADS), 0, stream, g, x);
+  if (b_type == T_F32) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_F32>, grid, dim3(MF_THREADS), 0, stream, g, x);
+  else if (b_type == T_BF16) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_BF16>, grid, dim3(MF_THREADS), 0, stream, g, x);
+  else hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_I8>, grid, dim3(MF_THREADS), 0, stream, g, x);
   return hipGetLastError();
 }
 

@@ -243,7 +243,7 @@ GEMV_NT_SHAPES = GEMV_SHAPES + [(1, 64, 128), (4, 65, 256), (1, 130, 200)]
 
 # 5 <= m <= 16 with whole 128-row leaves: the matrix-core skinny kernel
 GEMV_MFMA_SHAPES = [(5, 257, 1024), (8, 300, 4096), (12, 64, 512), (16, 1024, 128), (16, 4100, 1024),
-                    (9, 1000, 3968), (16, 14336, 4096)]
+                    (9, 1000, 3968), (16, 14336, 4096), (7, 200, 1664), (16, 96, 1152)]
 
 
 @pytest.mark.parametrize("kind", ["wide", "special"])
