@@ -48,7 +48,12 @@ struct GemvArgs {
 // cores (gemv_mfma.hip; X 16-byte aligned, 16 * K * 4 < 2^31).  Its workgroups are twice as
 // wide: MF_LEAVES leaves (an aligned subtree of 8) per workgroup, so the cross-workgroup fold
 // has half the roots.
-constexpr int GV_MFMA_MIN_M = 5;
+constexpr int GV_MFMA_MIN_M = 9;
+// ... and from this many rows up to GV_MFMA4_MAX_M, on the 4 x 4 shape.
+constexpr int GV_MFMA4_MIN_M = 3;
+constexpr int GV_MFMA4_MAX_M = 8;
+constexpr int MF4_LEAVES = 8;  // leaves per workgroup of the 4 x 4 kernel
+constexpr int MF4_THREADS = 64 * MF4_LEAVES;
 constexpr int MF_THREADS = 512;
 constexpr int MF_LEAVES = MF_THREADS / 64;
 
@@ -56,6 +61,9 @@ constexpr int MF_LEAVES = MF_THREADS / 64;
 hipError_t launch_gemv_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,
                           hipStream_t stream);
 hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, dim3 grid, hipStream_t stream);
+// 2 <= m <= 8 on the 4 x 4 shape (same conditions as the 16 x 16 kernel).
+hipError_t launch_gemv_mfma4_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, dim3 grid,
+                                hipStream_t stream);
 // vec (OP_NT): 0 element loads, 1 16-byte loads.
 hipError_t launch_gemv_nt(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,
                           hipStream_t stream);

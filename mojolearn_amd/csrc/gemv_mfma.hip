@@ -142,6 +142,152 @@ __global__ void __launch_bounds__(MF_THREADS) gemv_mfma_nn_kernel(GemvArgs g, co
   gv_finish<MR, COLS, MF_LEAVES, MF_THREADS>(g, part, last_flag, tid, grp, cg, m);
 }
 
+// ---- 2 <= M <= 8 on v_mfma_f32_4x4x1_16b_f32: sixteen 4 x 4 blocks with K = 1, one fma_rn
+// per output element like the other K = 1 shapes.  Output lane l, register r holds
+// A[lane 4 (l / 4) + r] * B[lane l] (+ C): lane l feeds A = x[4 g + l % 4][p] (its block's four
+// lanes carry rows 4g .. 4g+3) and B = W[p][CPL l + e], and gets column CPL l + e of those four
+// rows back.  G groups of four rows, CPL instructions per group per k step: no row is wasted
+// below M = 4 (the 16 x 16 shape computes 16).
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int BT, int G>
+__device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
+                                              int rowbytes, const float* __restrict__ xl, int64_t k, int m, float* xs,
+                                              int lane, const float (&sc)[GvCols<BT>::cpl]) {
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int NBLK = GV_CH / MF_RB;
+  constexpr int RING = MF_AHEAD + 1;
+  // x rows 0 .. 4G-1 (rows past m repeat row m-1) by the leaf's 128 steps into xs[4G][GV_CH]:
+  // 32 f4 a row, 2G f4 a lane (x + kb is 16-byte aligned, k a multiple of 128)
+#pragma unroll
+  for (int c = 0; c < 2 * G; ++c) {
+    const int idx = lane + 64 * c;
+    const int r = idx >> 5, q = idx & 31;
+    const f4 v = reinterpret_cast<const f4*>(xl + (int64_t)(r < m ? r : m - 1) * k)[q];
+    reinterpret_cast<f4*>(xs + r * GV_CH)[q] = v;
+  }
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
+  uint32_t ring[RING][MF_RB];
+#pragma unroll
+  for (int b = 0; b < MF_AHEAD; ++b)
+#pragma unroll
+    for (int i = 0; i < MF_RB; ++i)
+      ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * MF_RB + i) * rowbytes, 0);
+  const f4* xrow[G];
+  f4 xc[G], xn[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    xrow[g] = reinterpret_cast<const f4*>(xs + (4 * g + (lane & 3)) * GV_CH);
+    xc[g] = xrow[g][0];
+  }
+#pragma unroll
+  for (int b = 0; b < NBLK; ++b) {
+    if (b + MF_AHEAD < NBLK) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < MF_RB; ++i)
+        ring[(b + MF_AHEAD) % RING][i] =
+            __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ((b + MF_AHEAD) * MF_RB + i) * rowbytes, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q0 = 0; q0 < MF_RB; q0 += 4) {
+      const int s0 = b * MF_RB + q0;
+      if (s0 + 4 < GV_CH) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) xn[g] = xrow[g][(s0 + 4) / 4];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float wv[CPL];
+        gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float xa = xc[g][q];
+#pragma unroll
+          for (int e = 0; e < CPL; ++e) {
+            if (s0 + q == 0) acc[g][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(xa, wv[e], v4f{}, 0, 0, 0);
+            else acc[g][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(xa, wv[e], acc[g][e], 0, 0, 0);
+          }
+        }
+      }
+      if (s0 + 4 < GV_CH) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) xc[g] = xn[g];
+      }
+    }
+  }
+}
+
+template <int BT, int G>
+__global__ void __launch_bounds__(MF4_THREADS) gemv_mfma4_nn_kernel(GemvArgs g, const float* __restrict__ x) {
+  constexpr int MR = 4 * G;
+  constexpr int CPL = GvCols<BT>::cpl;
+  constexpr int COLS = GvCols<BT>::cols;
+  constexpr int EB = Elem<BT>::bytes;
+  constexpr int XS = MR * GV_CH;  // floats of one wave's x block
+  __shared__ __attribute__((aligned(16))) float part[MF4_LEAVES][MR][COLS];
+  __shared__ __attribute__((aligned(16))) float xown[MF4_LEAVES][XS];
+  __shared__ unsigned int last_flag;
+
+  set_flush_inputs_mode();
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t cg = blockIdx.x % g.ncg;
+  const int64_t grp = blockIdx.x / g.ncg;
+  const int64_t t = grp * MF4_LEAVES + wave;  // this wave's leaf
+  const int m = (int)g.m;
+
+  v4f acc[G][CPL];
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) acc[gg][e] = v4f{};
+
+  if (t < g.nleaves) {
+    // this lane's columns, clamped into the operand (their cells are never stored)
+    int64_t c0 = cg * COLS + lane * CPL;
+    if (c0 >= g.n) c0 = g.n - CPL;
+    float sc[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      sc[e] = 1.f;
+      if constexpr (BT == T_I8) sc[e] = g.scales[c0 + e];
+    }
+    const int64_t rowbytes = g.n * EB;
+    const int64_t kb = t * GV_CH;
+    gv_leaf_mfma4<BT, G>(acc, static_cast<const char*>(g.w) + kb * rowbytes, (uint32_t)(c0 * EB), (int)rowbytes,
+                         x + kb, g.k, m, &xown[wave][0], lane, sc);
+  }
+
+  // lane l: rows 4 gg + r of column CPL l + e in acc[gg][e][r]
+#pragma unroll
+  for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[wave][4 * gg + r][CPL * lane + e] = acc[gg][e][r];
+  gv_finish<MR, COLS, MF4_LEAVES, MF4_THREADS>(g, part, last_flag, tid, grp, cg, m);
+}
+
+hipError_t launch_gemv_mfma4_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, dim3 grid,
+                                hipStream_t stream) {
+  const bool two = m > 4;
+#define MLG_MF4(BT)                                                                                          \
+  do {                                                                                                       \
+    if (two) hipLaunchKernelGGL((gemv_mfma4_nn_kernel<BT, 2>), grid, dim3(MF4_THREADS), 0, stream, g, x);    \
+    else hipLaunchKernelGGL((gemv_mfma4_nn_kernel<BT, 1>), grid, dim3(MF4_THREADS), 0, stream, g, x);        \
+  } while (0)
+  if (b_type == T_F32) MLG_MF4(T_F32);
+  else if (b_type == T_BF16) MLG_MF4(T_BF16);
+  else MLG_MF4(T_I8);
+#undef MLG_MF4
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, dim3 grid, hipStream_t stream) {
   if (b_type == T_F32) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_F32>, grid, dim3(MF_THREADS), 0, stream, g, x);
   else if (b_type == T_BF16) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_BF16>, grid, dim3(MF_THREADS), 0, stream, g, x);

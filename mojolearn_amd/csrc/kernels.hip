@@ -130,12 +130,16 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
     const int64_t grid = v.ncg * v.ngroups;
     if (p.op == OP_NT)
       return launch_gemv_nt(v, static_cast<const float*>(p.a), p.b_type, p.m, vec - 3, dim3((unsigned)grid), stream);
-    if (vec == 2 && p.m >= GV_MFMA_MIN_M && aligned(p.a, 16) && 16 * p.k * 4 < (int64_t(1) << 31)) {
-      // fewer, wider groups (at most the workspace and counters sized for gemv_groups)
+    if (vec == 2 && p.m >= GV_MFMA4_MIN_M && aligned(p.a, 16) && 16 * p.k * 4 < (int64_t(1) << 31)) {
+      // the matrix-core kernels: fewer, wider groups (at most the workspace and counters sized
+      // for gemv_groups)
       GemvArgs vm = v;
-      vm.ngroups = (P + MF_LEAVES - 1) / MF_LEAVES;
-      return launch_gemv_mfma_nn(vm, static_cast<const float*>(p.a), p.b_type, dim3((unsigned)(vm.ncg * vm.ngroups)),
-                                 stream);
+      const bool four = p.m <= GV_MFMA4_MAX_M;
+      const int leaves = four ? MF4_LEAVES : MF_LEAVES;
+      vm.ngroups = (P + leaves - 1) / leaves;
+      const dim3 mgrid((unsigned)(vm.ncg * vm.ngroups));
+      if (four) return launch_gemv_mfma4_nn(vm, static_cast<const float*>(p.a), p.b_type, p.m, mgrid, stream);
+      return launch_gemv_mfma_nn(vm, static_cast<const float*>(p.a), p.b_type, mgrid, stream);
     }
     return launch_gemv_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, vec, dim3((unsigned)grid), stream);
   }

@@ -241,16 +241,18 @@ def test_skinny_m(oracle, shape, wt):
 
 GEMV_NT_SHAPES = GEMV_SHAPES + [(1, 64, 128), (4, 65, 256), (1, 130, 200)]
 
-# 5 <= m <= 16 with whole 128-row leaves: the matrix-core skinny kernel
+# 3 <= m <= 16 with whole 128-row leaves: the matrix-core skinny kernels (4 x 4 shape up to m = 8)
 GEMV_MFMA_SHAPES = [(5, 257, 1024), (8, 300, 4096), (12, 64, 512), (16, 1024, 128), (16, 4100, 1024),
-                    (9, 1000, 3968), (16, 14336, 4096), (7, 200, 1664), (16, 96, 1152)]
+                    (9, 1000, 3968), (16, 14336, 4096), (7, 200, 1664), (16, 96, 1152), (2, 300, 1024),
+                    (3, 257, 4096), (4, 14336, 4096), (6, 129, 1152), (4, 64, 640)]
 
 
 @pytest.mark.parametrize("kind", ["wide", "special"])
 @pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
 @pytest.mark.parametrize("shape", GEMV_MFMA_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_MFMA_SHAPES])
 def test_skinny_m_mfma(oracle, shape, wt, kind):
-    """5 <= m <= 16, whole leaves: the chains on v_mfma_f32_16x16x1_4b_f32 (one fma per step per
+    """3 <= m <= 16, whole leaves: the chains on v_mfma_f32_4x4x1_16b_f32 (m <= 8) or
+    v_mfma_f32_16x16x1_4b_f32 (one fma per step per
     cell, input flush by the mode), ragged column groups, one to many leaf groups, subnormal,
     signed-zero, inf and NaN operands, and the fused bias."""
     D = _dev()
