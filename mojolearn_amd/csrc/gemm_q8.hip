@@ -244,6 +244,73 @@ __global__ void q8_reduce_kernel(float* c, const int32_t* part, const int32_t* e
   c[i] = q8_dequant(acc, (int64_t)ea[i / n] + eb[i % n]);
 }
 
+// ---------------------------------------------------------------------------
+// Few rows of A (m <= 4): a streaming dot product per cell.  Each wave owns QV_ROWS rows of B
+// (qb[n][k], contiguous in k) and every row of A; lane l reads bytes 16 l .. 16 l + 15 of each
+// 1024-byte chunk of those rows (a row's chunk is one coalesced 1 KB read) and accumulates them
+// with v_dot4_i32_i8, then the 64 lane sums of a cell are added across the wave.  An Int32 sum of
+// int8 products below k = 131072 is exact in any order, so the cell is the oracle's Int32.  The
+// rows are bounded by their buffer resources (bytes past k read as zero codes).
+constexpr int QV_THREADS = 256;
+constexpr int QV_ROWS = 4;
+constexpr int QV_MAXM = 4;  // beyond, the matrix-unit tiles are faster (t8 rows)
+
+template <int MR>
+__global__ void __launch_bounds__(QV_THREADS) q8_gemv_kernel(float* c, const int8_t* qa, const int32_t* ea,
+                                                             const int8_t* qb, const int32_t* eb, int64_t m,
+                                                             int64_t n, int64_t k) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (QV_THREADS / 64) + (threadIdx.x >> 6);
+  const int64_t j0 = wave * QV_ROWS;
+  if (j0 >= n) return;  // whole waves only: nothing after this point synchronizes
+  __amdgpu_buffer_rsrc_t rb[QV_ROWS], ra[MR];
+#pragma unroll
+  for (int r = 0; r < QV_ROWS; ++r) {
+    const int64_t j = j0 + r < n ? j0 + r : n - 1;  // rows past n: loaded, never stored
+    rb[r] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qb + j * k), (short)0, (int)k, RSRC_WORD3);
+  }
+#pragma unroll
+  for (int i = 0; i < MR; ++i) {
+    const int64_t ii = i < m ? i : m - 1;  // rows past m: computed, never stored
+    ra[i] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qa + ii * k), (short)0, (int)k, RSRC_WORD3);
+  }
+  int32_t acc[MR][QV_ROWS];
+#pragma unroll
+  for (int i = 0; i < MR; ++i)
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r) acc[i][r] = 0;
+  for (int kc = 0; kc < (int)k; kc += 1024) {
+    const int off = kc + 16 * lane;
+    v4i w[QV_ROWS], a[MR];
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r) w[r] = __builtin_amdgcn_raw_buffer_load_b128(rb[r], off, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MR; ++i) a[i] = __builtin_amdgcn_raw_buffer_load_b128(ra[i], off, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MR; ++i)
+#pragma unroll
+      for (int r = 0; r < QV_ROWS; ++r)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[i][r] = __builtin_amdgcn_sdot4(a[i][d], w[r][d], acc[i][r], false);
+  }
+  // the wave's sum of each cell, then lane i * QV_ROWS + r stores cell (i, j0 + r)
+#pragma unroll
+  for (int i = 0; i < MR; ++i)
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r) {
+      int32_t v = acc[i][r];
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh, 64);
+      acc[i][r] = v;
+    }
+#pragma unroll
+  for (int i = 0; i < MR; ++i)
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r)
+      if (lane == i * QV_ROWS + r && i < m && j0 + r < n)
+        c[i * n + j0 + r] = q8_dequant(acc[i][r], (int64_t)ea[i] + eb[j0 + r]);
+}
+
 __global__ void q8_repack_kernel(int8_t* dst, const int8_t* src, int64_t rows, int64_t k, int64_t pitch) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= rows * pitch) return;
@@ -527,6 +594,7 @@ static int64_t q8_splits(int64_t m, int64_t n, int64_t k, int num_cus, int64_t* 
 static int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
 
 int64_t q8_workspace_bytes(const void* qa, const void* qb, int64_t m, int64_t n, int64_t k, int num_cus) {
+  if (m <= QV_MAXM && q8_in_place(qa, k) && q8_in_place(qb, k)) return 0;  // the streaming kernel
   int64_t bytes = 0;
   if (!q8_in_place(qa, k)) bytes += round256(m * q8_pitch(k));
   if (!q8_in_place(qb, k)) bytes += round256(n * q8_pitch(k));
@@ -555,6 +623,16 @@ hipError_t run_q8_dequantize(float* out, const int8_t* codes, const int32_t* exp
 hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8_t* qb, const int32_t* eb,
                        int64_t m, int64_t n, int64_t k, void* ws, int num_cus, hipStream_t stream) {
   if (m <= 0 || n <= 0 || k <= 0 || k > INT8_MAX_K) return hipErrorInvalidValue;
+  if (m <= QV_MAXM && q8_in_place(qa, k) && q8_in_place(qb, k)) {
+    const unsigned grid = (unsigned)((n + QV_ROWS * (QV_THREADS / 64) - 1) / (QV_ROWS * (QV_THREADS / 64)));
+#define MLG_QV(MR) hipLaunchKernelGGL(q8_gemv_kernel<MR>, dim3(grid), dim3(QV_THREADS), 0, stream, c, \
+                                      static_cast<const int8_t*>(qa), ea, static_cast<const int8_t*>(qb), eb, m, n, k)
+    if (m == 1) MLG_QV(1);
+    else if (m == 2) MLG_QV(2);
+    else MLG_QV(4);
+#undef MLG_QV
+    return hipGetLastError();
+  }
   const int64_t pitch = q8_pitch(k);
   if (32 * pitch + Q8_KS >= (int64_t(1) << 30)) return hipErrorInvalidValue;
   char* wsp = static_cast<char*>(ws);
