@@ -696,8 +696,11 @@ hipError_t run_q15_dequantize(float* out, const int8_t* hi, const int8_t* lo, co
 static bool q15_in_place(const void* p, int64_t k) { return k % Q15_KS == 0 && ((uintptr_t)p % 16u) == 0; }
 static int64_t q15_pitch(int64_t k) { return (k + Q15_KS - 1) / Q15_KS * Q15_KS; }
 
+static bool q15_streams(const void* ah, const void* al, const void* bh, const void* bl, int64_t m, int64_t k);
+
 int64_t q15_workspace_bytes(const void* ah, const void* al, const void* bh, const void* bl, int64_t m, int64_t n,
                             int64_t k, int num_cus) {
+  if (q15_streams(ah, al, bh, bl, m, k)) return 0;  // the streaming kernel
   int64_t bytes = 0;
   if (!q15_in_place(ah, k) || !q15_in_place(al, k)) bytes += 2 * round256(m * q15_pitch(k));
   if (!q15_in_place(bh, k) || !q15_in_place(bl, k)) bytes += 2 * round256(n * q15_pitch(k));
@@ -707,10 +710,102 @@ int64_t q15_workspace_bytes(const void* ah, const void* al, const void* bh, cons
   return bytes;
 }
 
+// Few rows of A (m <= 4) under int15i64: the streaming kernel of the int8 product on both planes
+// of A and B, the three Int32 sums of W-5 per cell (HH = ah.bh, MID = ah.bl + al.bh, LL = al.bl),
+// each exact in any order below k = 65536 (|partial sums| stay under the contract's bound), then
+// the cell's Int64 recombination and W-6 conversion.
+template <int MR>
+__global__ void __launch_bounds__(QV_THREADS) q15_gemv_kernel(float* c, const int8_t* ah, const int8_t* al,
+                                                              const int32_t* ea, const int8_t* bh, const int8_t* bl,
+                                                              const int32_t* eb, int64_t m, int64_t n, int64_t k) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (QV_THREADS / 64) + (threadIdx.x >> 6);
+  const int64_t j0 = wave * QV_ROWS;
+  if (j0 >= n) return;  // whole waves only: nothing after this point synchronizes
+  __amdgpu_buffer_rsrc_t rbh[QV_ROWS], rbl[QV_ROWS], rah[MR], ral[MR];
+#pragma unroll
+  for (int r = 0; r < QV_ROWS; ++r) {
+    const int64_t j = j0 + r < n ? j0 + r : n - 1;  // rows past n: loaded, never stored
+    rbh[r] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(bh + j * k), (short)0, (int)k, RSRC_WORD3);
+    rbl[r] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(bl + j * k), (short)0, (int)k, RSRC_WORD3);
+  }
+#pragma unroll
+  for (int i = 0; i < MR; ++i) {
+    const int64_t ii = i < m ? i : m - 1;  // rows past m: computed, never stored
+    rah[i] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(ah + ii * k), (short)0, (int)k, RSRC_WORD3);
+    ral[i] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(al + ii * k), (short)0, (int)k, RSRC_WORD3);
+  }
+  int32_t hh[MR][QV_ROWS], mid[MR][QV_ROWS], ll[MR][QV_ROWS];
+#pragma unroll
+  for (int i = 0; i < MR; ++i)
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r) hh[i][r] = mid[i][r] = ll[i][r] = 0;
+  for (int kc = 0; kc < (int)k; kc += 1024) {
+    const int off = kc + 16 * lane;
+    v4i wh[QV_ROWS], wl[QV_ROWS], xh[MR], xl[MR];
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r) {
+      wh[r] = __builtin_amdgcn_raw_buffer_load_b128(rbh[r], off, 0, 0);
+      wl[r] = __builtin_amdgcn_raw_buffer_load_b128(rbl[r], off, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      xh[i] = __builtin_amdgcn_raw_buffer_load_b128(rah[i], off, 0, 0);
+      xl[i] = __builtin_amdgcn_raw_buffer_load_b128(ral[i], off, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i)
+#pragma unroll
+      for (int r = 0; r < QV_ROWS; ++r)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          hh[i][r] = __builtin_amdgcn_sdot4(xh[i][d], wh[r][d], hh[i][r], false);
+          mid[i][r] = __builtin_amdgcn_sdot4(xh[i][d], wl[r][d], mid[i][r], false);
+          mid[i][r] = __builtin_amdgcn_sdot4(xl[i][d], wh[r][d], mid[i][r], false);
+          ll[i][r] = __builtin_amdgcn_sdot4(xl[i][d], wl[r][d], ll[i][r], false);
+        }
+  }
+#pragma unroll
+  for (int i = 0; i < MR; ++i)
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r) {
+      int32_t a = hh[i][r], b = mid[i][r], d = ll[i][r];
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) {
+        a += __shfl_xor(a, sh, 64);
+        b += __shfl_xor(b, sh, 64);
+        d += __shfl_xor(d, sh, 64);
+      }
+      hh[i][r] = a;
+      mid[i][r] = b;
+      ll[i][r] = d;
+    }
+#pragma unroll
+  for (int i = 0; i < MR; ++i)
+#pragma unroll
+    for (int r = 0; r < QV_ROWS; ++r)
+      if (lane == i * QV_ROWS + r && i < m && j0 + r < n)
+        c[i * n + j0 + r] = q15_cell(hh[i][r], mid[i][r], ll[i][r], (int64_t)ea[i] + eb[j0 + r]);
+}
+
+static bool q15_streams(const void* ah, const void* al, const void* bh, const void* bl, int64_t m, int64_t k) {
+  return m <= QV_MAXM && q8_in_place(ah, k) && q8_in_place(al, k) && q8_in_place(bh, k) && q8_in_place(bl, k);
+}
+
 hipError_t run_q15_gemm(float* c, const int8_t* ah, const int8_t* al, const int32_t* ea, const int8_t* bh,
                         const int8_t* bl, const int32_t* eb, int64_t m, int64_t n, int64_t k, void* ws, int num_cus,
                         hipStream_t stream) {
   if (m <= 0 || n <= 0 || k <= 0 || k > INT15_MAX_K_DEV) return hipErrorInvalidValue;
+  if (q15_streams(ah, al, bh, bl, m, k)) {
+    const unsigned grid = (unsigned)((n + QV_ROWS * (QV_THREADS / 64) - 1) / (QV_ROWS * (QV_THREADS / 64)));
+#define MLG_QV15(MR) hipLaunchKernelGGL(q15_gemv_kernel<MR>, dim3(grid), dim3(QV_THREADS), 0, stream, c, ah, al, ea, \
+                                        bh, bl, eb, m, n, k)
+    if (m == 1) MLG_QV15(1);
+    else if (m == 2) MLG_QV15(2);
+    else MLG_QV15(4);
+#undef MLG_QV15
+    return hipGetLastError();
+  }
   const int64_t pitch = q15_pitch(k);
   if (32 * pitch + Q15_KS >= (int64_t(1) << 30)) return hipErrorInvalidValue;
   char* wsp = static_cast<char*>(ws);

@@ -48,7 +48,8 @@ def _run(oracle, qa, qb, ea, eb, what):
 # (1, 4096, 4096), (8, 300, 14336), (33, 47, 65536) and (16, 129, 385) split k;
 # k % 64 != 0 takes the repack
 SHAPES = [(1, 1, 1), (3, 5, 7), (130, 129, 64), (128, 128, 128), (129, 257, 129), (200, 300, 4097),
-          (64, 1000, 520), (512, 512, 512), (1, 4096, 4096), (8, 300, 14336), (33, 47, 65536), (16, 129, 385)]
+          (64, 1000, 520), (512, 512, 512), (1, 4096, 4096), (8, 300, 14336), (33, 47, 65536), (16, 129, 385),
+          (2, 77, 1024), (3, 333, 2064), (4, 4096, 4096), (1, 129, 4112), (4, 3, 65536)]
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in SHAPES])
