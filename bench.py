@@ -5,8 +5,11 @@ Headline (the JSON line's `value`): the decoder-LM prefill projection, X[2048x40
 inputs resident in HBM, one product per step, in TFLOP/s (2mnk per step; the bias adds are not
 counted).  Beside it: the kernel's roofline fraction (FP32 matrix peak 157.3 TFLOP/s), the
 other workloads (--all: 512^3, decode GEMV with an int8 weight at M = 1/4/16 in GB/s, the bf16
-SwiGLU up projection, the adversarial LM head), the mismatching words against the CPU oracle on
-sampled rows, and the CPU oracle timed on the host cores.
+SwiGLU up projection, the adversarial LM head, and one GPU's N/8 column shard of the decode GEMV
+and of the prefill, each the median of 20 timed runs with the fastest and slowest), the
+mismatching words against the CPU oracle on sampled rows, and the CPU oracle timed on the host
+cores (with --all, both arms on every workload: the scalar oracle on one thread, the fast one
+on every thread, and the host's CPU).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
 """
@@ -28,23 +31,27 @@ HBM_PEAK_GBS = 8000.0
 EAGER = False  # --eager: time plain launches instead of graph replays (for counter runs)
 
 
-def graph_time(calls, steps, warmup, torch):
-    """Average ms per call: `steps` calls (round-robin over `calls`, each a Plan) captured in one
-    HIP graph on a private stream and replayed; HIP events on the replaying stream.  With
-    EAGER the same calls are launched one by one on that stream, bracketed by its events."""
+def graph_runs(calls, steps, warmup, torch, runs=1):
+    """Average ms per call of each of `runs` timed runs: `steps` calls (round-robin over `calls`,
+    each a Plan) captured in one HIP graph on a private stream, replayed once per run; HIP events
+    on the replaying stream.  With EAGER the same calls are launched one by one on that stream,
+    bracketed by its events."""
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         for i in range(max(warmup, len(calls))):
             calls[i % len(calls)](s)
     torch.cuda.synchronize()
+    out = []
     if EAGER:
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for i in range(steps):
-            calls[i % len(calls)](s)
-        e1.record(s)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / steps
+        for _ in range(runs):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(steps):
+                calls[i % len(calls)](s)
+            e1.record(s)
+            e1.synchronize()
+            out.append(e0.elapsed_time(e1) / steps)
+        return out
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for i in range(steps):
@@ -52,12 +59,27 @@ def graph_time(calls, steps, warmup, torch):
     g.replay()
     torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(cur)
-    g.replay()
-    e1.record(cur)
-    e1.synchronize()
-    return e0.elapsed_time(e1) / steps
+    for _ in range(runs):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        g.replay()
+        e1.record(cur)
+        e1.synchronize()
+        out.append(e0.elapsed_time(e1) / steps)
+    return out
+
+
+def graph_time(calls, steps, warmup, torch):
+    """Average ms per call over one timed run of `steps` calls (graph_runs)."""
+    return graph_runs(calls, steps, warmup, torch)[0]
+
+
+def _timed(calls, steps, warmup, torch, runs):
+    """{"ms": ...} from one run, or with runs > 1 the median run and the fastest and slowest."""
+    t = sorted(graph_runs(calls, steps, warmup, torch, runs))
+    if runs == 1:
+        return {"ms": t[0]}
+    return {"ms": float(np.median(t)), "ms_min": t[0], "ms_max": t[-1], "runs": runs}
 
 
 PREFILL_PROFILE = os.path.join(ROOT, "profiles", "gemm_mfma_kernel_prefill_2048x4096x4096.md")
@@ -91,13 +113,18 @@ def _t(torch, x):
     return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
 
 
-def bench_prefill(torch, D, W, O, steps, warmup, check):
+def bench_prefill(torch, D, W, O, steps, warmup, check, runs=1, cols=None):
+    """The prefill projection; `cols` keeps W's and bias's first columns (one GPU's column
+    shard at its real shape)."""
     x, w, bias = W.prefill()
+    if cols is not None:
+        w, bias = np.ascontiguousarray(w[:, :cols]), np.ascontiguousarray(bias[:cols])
     plan = D.Plan(_t(torch, x), _t(torch, w), bias=_t(torch, bias))
-    ms = graph_time([plan], steps, warmup, torch)
+    res = _timed([plan], steps, warmup, torch, runs)
+    ms = res["ms"]
     m, k = x.shape
     n = w.shape[1]
-    res = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+    res["tflops"] = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     if check:
         rows = _rows(m)
         want = O.nan_canon(O.bias(O.gemm_fast(x[rows], w, 0), bias))
@@ -106,14 +133,15 @@ def bench_prefill(torch, D, W, O, steps, warmup, check):
     return res
 
 
-def bench_product(torch, D, a, b, steps, warmup, want_fn=None):
+def bench_product(torch, D, a, b, steps, warmup, want_fn=None, runs=1):
     """One Plan (a: float32, b: float32 or bf16 bits as uint16) timed as graph replays."""
     tb = _t(torch, b.view(np.int16) if b.dtype == np.uint16 else b)
     plan = D.Plan(_t(torch, a), tb)
-    ms = graph_time([plan], steps, warmup, torch)
+    res = _timed([plan], steps, warmup, torch, runs)
+    ms = res["ms"]
     m, k = a.shape
     n = b.shape[1]
-    res = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+    res["tflops"] = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     if want_fn is not None:
         rows = _rows(m)
         res["mismatched_words"] = _mismatch(plan.out.cpu().numpy()[rows], want_fn(rows))
@@ -121,25 +149,32 @@ def bench_product(torch, D, a, b, steps, warmup, want_fn=None):
     return res
 
 
-def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8):
-    """int8-weight GEMV; `nbuf` distinct weight buffers (8 x 58.7 MB > the 256 MB Infinity
-    Cache) rotate so W streams from HBM.  GB/s counts K*N int8 codes + N scales + M*K x +
-    M*N y per call."""
+def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=None, wdeq=None):
+    """int8-weight GEMV; `nbuf` distinct weight buffers rotate so W streams from HBM (8 x 58.7
+    MB > the 256 MB Infinity Cache; a column shard rotates enough copies to exceed it too).
+    GB/s counts K*N int8 codes + N scales + M*K x + M*N y per call.  `cols` keeps the first
+    columns (one GPU's column shard); `wdeq` is the oracle's dequantized W when already made."""
     x16, codes, scales = W.decode()
+    if cols is not None:
+        codes, scales = np.ascontiguousarray(codes[:, :cols]), np.ascontiguousarray(scales[:cols])
+        nbuf = max(nbuf, -(-(320 << 20) // codes.size))
     x = np.ascontiguousarray(x16[:m])
     tx, ts = _t(torch, x), _t(torch, scales)
     out = torch.empty((m, codes.shape[1]), dtype=torch.float32, device="cuda:0")
     tcodes = [_t(torch, codes)] + [_t(torch, np.roll(codes, i, axis=1)) for i in range(1, nbuf)]
     plans = [D.Plan(tx, tc, scales=ts, out=out) for tc in tcodes]
-    ms = graph_time(plans, max(steps, 2 * nbuf), warmup, torch)
+    res = _timed(plans, max(steps, 2 * nbuf), warmup, torch, runs)
+    ms = res["ms"]
     k, n = codes.shape
     nbytes = k * n + 4 * n + 4 * m * k + 4 * m * n
-    res = {"ms": ms, "us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
-           "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-           "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "bytes": nbytes}
+    res.update({"us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "bytes": nbytes})
     if check:
         plans[0]()
-        want = O.gemm_fast(x, O.int8_dequant(codes, scales, 0), 0)
+        if wdeq is None:
+            wdeq = O.int8_dequant(codes, scales, 0)
+        want = O.gemm_fast(x, np.ascontiguousarray(wdeq[:, :n]), 0)
         res["mismatched_words"] = _mismatch(out.cpu().numpy(), want)
         res["checked_cells"] = int(m * n)
     return res
@@ -164,6 +199,78 @@ def cpu_baseline(W, O, min_seconds=10.0, max_seconds=30.0):
             "kind": "port",
             "sample": f"the whole prefill product (X[2048x4096] . W[4096x4096] + bias) x {reps}, "
                       f"oracle/gemm_oracle.c fast arm (AVX2 FMA), {threads} threads, {dt:.1f} s"}
+
+
+#: The reference's host budget for its scalar oracle arm, in multiply-accumulates
+#: (bench/gemm_card_main.mojo:241), and its rule for meeting it (:361-378): halve n (or m, when
+#: m > n) until m*n*k fits; k is never touched, so every cell keeps its leaves and tree.
+HOST_MAC_BUDGET = 16_000_000
+
+
+def host_capped(m, n, k):
+    while m * n * k > HOST_MAC_BUDGET and (m > 1 or n > 1):
+        if n >= m and n > 1:
+            n = (n + 1) // 2
+        else:
+            m = (m + 1) // 2
+    return m, n
+
+
+def host_info():
+    """The host's CPU: the threads this process may use and the model name."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": len(os.sched_getaffinity(0)), "cpu_count": os.cpu_count(), "model": model}
+
+
+def cpu_arms(W, O):
+    """Both CPU arms on the five workloads, timed on this host: (i) the scalar oracle (the
+    reference's CPU binding's algorithm) on one thread, full size for 512^3 and the decode GEMV,
+    capped by the reference's host budget for the three large products; (ii) the fast oracle
+    (AVX2 FMA) on every host thread, full size.  Where an arm ran a capped block, its bits are
+    compared with the same block of the fast arm's full output (a cell's arithmetic depends on
+    k only, so the block must match word for word)."""
+    threads = O.max_threads()
+    rows = {}
+
+    def arm(fn, m, n, k):
+        t0 = time.perf_counter()
+        y = fn()
+        dt = time.perf_counter() - t0
+        return y, {"shape": [m, n, k], "s": dt, "gflops": 2.0 * m * n * k / dt / 1e9}
+
+    def both(name, a, b, post=None, full=False):
+        m, k = a.shape
+        n = b.shape[1]
+        post = post or (lambda y, cols: y)
+        fast, rf = arm(lambda: post(O.gemm_fast(a, b, 0, threads=threads), n), m, n, k)
+        mm, nn = (m, n) if full else host_capped(m, n, k)
+        sa, sb = np.ascontiguousarray(a[:mm]), np.ascontiguousarray(b[:, :nn])
+        scal, rs = arm(lambda: post(O.gemm(sa, sb, 0), nn), mm, nn, k)
+        rs["capped"] = (mm, nn) != (m, n)
+        rs["mismatched_words_vs_fast"] = _mismatch(scal, fast[:mm, :nn])
+        rows[name] = {"scalar_1_thread": rs, "fast_all_threads": rf}
+
+    a, b = W.gemm512()
+    both("gemm512", a, b, full=True)
+    x, w, bias = W.prefill()
+    both("prefill", x, w, post=lambda y, cols: O.bias(y, bias[:cols]))
+    x16, codes, scales = W.decode()
+    wdeq = O.int8_dequant(codes, scales, 0)
+    for m in (1, 4, 16):
+        both(f"decode_m{m}", np.ascontiguousarray(x16[:m]), wdeq, full=True)
+    x, wb = W.swiglu_up()
+    both("swiglu_up", x, O.bf16_widen(wb))
+    x, w = W.lm_head()
+    both("lm_head", x, w, post=lambda y, cols: O.nan_canon(y))
+    return {"host": host_info(), "threads": threads, "rows": rows}
 
 
 def bench_compare(torch, D, steps, warmup):
@@ -376,19 +483,33 @@ def main():
     pre = bench_prefill(torch, D, W, O, args.steps, args.warmup, check)
     extra = {}
     if args.all:
+        # every row: the median of RUNS timed runs (graph replays), with the fastest and slowest
+        R = 20
+        extra["prefill"] = bench_prefill(torch, D, W, O, args.steps, args.warmup, check, runs=R)
         a, b = W.gemm512()
         extra["gemm512"] = bench_product(torch, D, a, b, args.steps, args.warmup,
-                                         want_fn=(lambda r: O.gemm(a[r], b, 0)) if check else None)
+                                         want_fn=(lambda r: O.gemm(a[r], b, 0)) if check else None, runs=R)
+        x16, codes, scales = W.decode()
+        wdeq = O.int8_dequant(codes, scales, 0) if check else None
+        del x16, codes, scales
         for m in (1, 4, 16):
-            extra[f"decode_m{m}"] = bench_decode(torch, D, W, O, m, args.steps, args.warmup, check)
+            extra[f"decode_m{m}"] = bench_decode(torch, D, W, O, m, args.steps, args.warmup, check, runs=R,
+                                                 wdeq=wdeq)
         x, wb = W.swiglu_up()
         extra["swiglu_up"] = bench_product(
-            torch, D, x, wb, max(3, args.steps // 4), 1,
-            want_fn=(lambda r: O.gemm_fast(x[r], O.bf16_widen(wb), 0)) if check else None)
+            torch, D, x, wb, max(3, args.steps // 4), max(3, args.warmup // 10),
+            want_fn=(lambda r: O.gemm_fast(x[r], O.bf16_widen(wb), 0)) if check else None, runs=R)
         x, w = W.lm_head()
         extra["lm_head"] = bench_product(
-            torch, D, x, w, max(3, args.steps // 2), 1,
-            want_fn=(lambda r: O.nan_canon(O.gemm_fast(x[r], w, 0))) if check else None)
+            torch, D, x, w, max(3, args.steps // 2), max(3, args.warmup // 4),
+            want_fn=(lambda r: O.nan_canon(O.gemm_fast(x[r], w, 0))) if check else None, runs=R)
+        del x, w, wb
+        # one GPU's share of the two products a column split spreads over 8 GPUs: N/8 columns
+        extra["shard_decode_m1_n1792"] = bench_decode(torch, D, W, O, 1, args.steps, args.warmup, check,
+                                                      runs=R, cols=14336 // 8, wdeq=wdeq)
+        extra["shard_prefill_n512"] = bench_prefill(torch, D, W, O, args.steps, args.warmup, check, runs=R,
+                                                    cols=4096 // 8)
+        del wdeq
 
     if args.compare:
         extra["compare"] = bench_compare(torch, D, args.steps, args.warmup)
@@ -428,6 +549,8 @@ def main():
         line["workloads"] = _round(extra)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(W, O)
+        if args.all:
+            line["cpu_arms"] = _round(cpu_arms(W, O))
     print(json.dumps(line), flush=True)
 
 

@@ -71,3 +71,34 @@ def test_lm_head_rows(oracle):
     want = oracle.nan_canon(oracle.gemm_fast(x[rows], w, 0))
     assert np.array_equal(_bits(y[rows]), _bits(want))
     assert np.isnan(y).any()  # the adversarial magnitudes do produce inf - inf
+
+
+@pytest.mark.parametrize("m", [1, 16])
+def test_decode_column_shards_concatenate_to_the_whole(oracle, m):
+    """A column split over 8 GPUs needs no arithmetic exchange: each GPU's N/8 columns (one
+    launch each, at the shard's own shape) are the whole product's bits."""
+    from mojolearn_amd import device as D
+    x16, codes, scales = W.decode()
+    x = np.ascontiguousarray(x16[:m])
+    tx = _t(x)
+    whole = D.gemm_int8w(tx, _t(codes), _t(scales)).cpu().numpy()
+    step = codes.shape[1] // 8
+    parts = [D.gemm_int8w(tx, _t(codes[:, s:s + step]), _t(scales[s:s + step])).cpu().numpy()
+             for s in range(0, codes.shape[1], step)]
+    assert np.array_equal(_bits(np.concatenate(parts, axis=1)), _bits(whole))
+    want = oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0)
+    assert np.array_equal(_bits(whole), _bits(want))
+
+
+def test_prefill_column_shards_concatenate_to_the_whole(oracle):
+    from mojolearn_amd import device as D
+    x, w, bias = W.prefill()
+    tx = _t(x)
+    whole = D.gemm(tx, _t(w), bias=_t(bias)).cpu().numpy()
+    step = w.shape[1] // 8
+    parts = [D.gemm(tx, _t(w[:, s:s + step]), bias=_t(bias[s:s + step])).cpu().numpy()
+             for s in range(0, w.shape[1], step)]
+    assert np.array_equal(_bits(np.concatenate(parts, axis=1)), _bits(whole))
+    rows = _rows(x.shape[0])
+    want = oracle.nan_canon(oracle.bias(oracle.gemm_fast(x[rows], w[:, :step], 0), bias[:step]))
+    assert np.array_equal(_bits(parts[0][rows]), _bits(want))
