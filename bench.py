@@ -31,23 +31,24 @@ HBM_PEAK_GBS = 8000.0
 EAGER = False  # --eager: time plain launches instead of graph replays (for counter runs)
 
 
-def graph_runs(calls, steps, warmup, torch, runs=1):
+def graph_runs(calls, steps, warmup, torch, runs=1, eager=None):
     """Average ms per call of each of `runs` timed runs: `steps` calls (round-robin over `calls`,
     each a Plan) captured in one HIP graph on a private stream, replayed once per run; HIP events
-    on the replaying stream.  With EAGER the same calls are launched one by one on that stream,
-    bracketed by its events."""
+    on the replaying stream.  With EAGER (or `eager`) the same calls are launched one by one on
+    that stream, bracketed by its events."""
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         for i in range(max(warmup, len(calls))):
             calls[i % len(calls)](s)
     torch.cuda.synchronize()
     out = []
-    if EAGER:
+    if EAGER or eager:
         for _ in range(runs):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-            for i in range(steps):
-                calls[i % len(calls)](s)
+            with torch.cuda.stream(s):
+                for i in range(steps):
+                    calls[i % len(calls)](s)
             e1.record(s)
             e1.synchronize()
             out.append(e0.elapsed_time(e1) / steps)
@@ -74,9 +75,9 @@ def graph_time(calls, steps, warmup, torch):
     return graph_runs(calls, steps, warmup, torch)[0]
 
 
-def _timed(calls, steps, warmup, torch, runs):
+def _timed(calls, steps, warmup, torch, runs, eager=None):
     """{"ms": ...} from one run, or with runs > 1 the median run and the fastest and slowest."""
-    t = sorted(graph_runs(calls, steps, warmup, torch, runs))
+    t = sorted(graph_runs(calls, steps, warmup, torch, runs, eager))
     if runs == 1:
         return {"ms": t[0]}
     return {"ms": float(np.median(t)), "ms_min": t[0], "ms_max": t[-1], "runs": runs}
@@ -199,6 +200,75 @@ def cpu_baseline(W, O, min_seconds=10.0, max_seconds=30.0):
             "kind": "port",
             "sample": f"the whole prefill product (X[2048x4096] . W[4096x4096] + bias) x {reps}, "
                       f"oracle/gemm_oracle.c fast arm (AVX2 FMA), {threads} threads, {dt:.1f} s"}
+
+
+class _SeqLinear:
+    """The sequence executor's linear step (sequence/ops.mojo:485-569): op_gemm, one whole-k chain
+    per cell into `out`, then the bias + activation follower over it."""
+
+    def __init__(self, torch, D, x, w, bias, act):
+        self.D, self.x, self.w, self.bias, self.act = D, x, w, bias, act
+        self.out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
+
+    def __call__(self, stream=None):
+        self.D.seq_gemm(self.x, self.w, self.out)
+        self.D.follow(self.out, self.D.EPI_BIAS_ACT, self.bias, self.act)
+
+
+class _SeqAccumulate:
+    """op_gemm with accumulate: the weight gradient dW += X^T . dY through strided views (X^T is X
+    read k-major, no copy), each chain seeded by the flushed old dW."""
+
+    def __init__(self, D, xt, dy, dw):
+        self.D, self.xt, self.dy, self.out = D, xt, dy, dw
+
+    def __call__(self, stream=None):
+        self.D.seq_gemm(self.xt, self.dy, self.out, accumulate=True)
+
+
+def bench_seq(torch, D, W, O, steps, warmup, check, runs=1):
+    """The sequence-executor word on the prefill operands, eager launches (HIP events on the
+    launching stream): the linear step X[2048x4096] . W[4096x4096], bias + ReLU, and the weight
+    gradient dW[4096x4096] += X^T . dY[2048x4096].  Sampled rows are checked against the
+    oracle's op_gemm and follower."""
+    x, w, bias = W.prefill()
+    m, k = x.shape
+    n = w.shape[1]
+    tx, tw, tb = _t(torch, x), _t(torch, w), _t(torch, bias)
+    out = {}
+    lin = _SeqLinear(torch, D, tx, tw, tb, D.ACT_RELU)
+    res = _timed([lin], max(3, steps // 2), max(3, warmup // 4), torch, runs, eager=True)
+    res["tflops"] = 2.0 * m * n * k / (res["ms"] * 1e-3) / 1e12
+    if check:
+        rows = _rows(m)
+        xr = np.ascontiguousarray(x[rows])
+        want = np.zeros((len(rows), n), np.float32)
+        O.seq_gemm(want, xr, w, len(rows), n, k, k, 1, n, 1, n, False)
+        O.epilogue(want, n, len(rows), n, O.EPI_BIAS_ACT, bias, O.ACT_RELU)
+        res["mismatched_words"] = _mismatch(lin.out.cpu().numpy()[rows], want)
+        res["checked_cells"] = int(len(rows) * n)
+    out["seq_linear_bias_relu_2048x4096x4096"] = res
+    del lin
+    dy = np.random.default_rng(5).standard_normal((m, n), dtype=np.float32)
+    tdy = _t(torch, dy)
+    dw0 = (np.random.default_rng(6).standard_normal((k, n), dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    tdw = _t(torch, dw0)
+    acc = _SeqAccumulate(D, tx.t(), tdy, tdw)
+    if check:
+        # one accumulation from a known dW, checked before the timed ones drift it further
+        acc()
+        rows = _rows(k)
+        want = np.ascontiguousarray(dw0[rows])
+        xt_rows = np.ascontiguousarray(x[:, rows].T)
+        O.seq_gemm(want, xt_rows, dy, len(rows), n, m, m, 1, n, 1, n, True)
+        mism = _mismatch(tdw.cpu().numpy()[rows], want)
+    res = _timed([acc], max(3, steps // 4), max(3, warmup // 10), torch, runs, eager=True)
+    res["tflops"] = 2.0 * k * n * m / (res["ms"] * 1e-3) / 1e12
+    if check:
+        res["mismatched_words"] = mism
+        res["checked_cells"] = int(len(rows) * n)
+    out["seq_grad_accumulate_4096x4096x2048"] = res
+    return out
 
 
 #: The reference's host budget for its scalar oracle arm, in multiply-accumulates
@@ -463,7 +533,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the product shards by output columns with no arithmetic exchange; see DESIGN.md)",
+              "(the product shards by output columns with no arithmetic exchange)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -510,6 +580,7 @@ def main():
         extra["shard_prefill_n512"] = bench_prefill(torch, D, W, O, args.steps, args.warmup, check, runs=R,
                                                     cols=4096 // 8)
         del wdeq
+        extra.update(bench_seq(torch, D, W, O, args.steps, args.warmup, check, runs=R))
 
     if args.compare:
         extra["compare"] = bench_compare(torch, D, args.steps, args.warmup)
