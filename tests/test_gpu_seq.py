@@ -173,3 +173,29 @@ def test_follower_derivatives_wide(oracle, act):
     torch.cuda.synchronize()
     want = oracle.epilogue(d.reshape(m, n).copy(), n, m, n, 5, z, act)
     _same(td.cpu().numpy(), want, f"derivative {act}")
+
+
+LAYOUTS = [(70000, 4, 4, 0), (33, 1028, 1036, 0), (33, 1030, 1036, 0), (33, 1028, 1030, 0), (33, 1028, 1036, 1),
+           (5, 3000, 3000, 0)]
+
+
+@pytest.mark.parametrize("epi,act", [(4, 1), (5, 2), (3, 0)], ids=["bias-logistic", "tanh-bwd", "bias"])
+@pytest.mark.parametrize("layout", LAYOUTS, ids=[f"{m}x{n}-ld{ld}-off{o}" for m, n, ld, o in LAYOUTS])
+def test_follower_layouts(oracle, layout, epi, act):
+    """The followers over views of every layout the launch distinguishes (more rows than one grid
+    dimension holds; row strides above n, not a multiple of 4; a base off 16 bytes): every cell
+    of the view against the oracle, every word outside it untouched."""
+    m, n, ldc, off = layout
+    print(f"follower layout {layout} epi={epi} act={act}", flush=True)
+    rng = np.random.default_rng(m + n + ldc + off + epi)
+    flat = (rng.standard_normal(off + m * ldc) * 4).astype(np.float32)
+    p = (rng.standard_normal(n) if epi != 5 else rng.uniform(-1, 1, m * n)).astype(np.float32)
+    tflat = torch.from_numpy(flat.copy()).to(DEV)
+    view = tflat[off:].view(m, ldc)[:, :n]
+    _dev().follow(view, epi, torch.from_numpy(p).to(DEV), act)
+    torch.cuda.synchronize()
+    want = flat.copy()
+    body = np.ascontiguousarray(want[off:])
+    oracle.epilogue(body, ldc, m, n, epi, p, act)
+    want[off:] = body
+    _same(tflat.cpu().numpy(), want, "buffer")
