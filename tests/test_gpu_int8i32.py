@@ -35,11 +35,12 @@ def _bits_equal(got, want, what):
 
 # (1, 4096, 4096), (8, 300, 14336), (3, 1000, 1000), (33, 47, 131072) and (16, 129, 385) split k;
 # m <= 4 with k a multiple of 16 and aligned rows takes the streaming kernel (the extreme codes of row 0
-# reach -127 * 127 * 131072 at k = 131072).
+# reach -127 * 127 * 131072 at k = 131072); m = 5..9 take the tiles with a partial tile of rows.
 SHAPES = [(1, 1, 1), (3, 5, 7), (1, 300, 16), (130, 129, 16), (128, 128, 128), (129, 257, 129),
           (200, 300, 4097), (64, 1000, 520), (300, 64, 2048), (33, 47, 131072), (512, 512, 512),
           (1, 4096, 4096), (8, 300, 14336), (3, 1000, 1000), (16, 129, 385), (2, 77, 1024), (3, 333, 2064),
-          (4, 14336, 4096), (4, 1, 131072), (1, 129, 4112), (1, 5, 131072), (7, 64, 2048)]
+          (4, 14336, 4096), (4, 1, 131072), (1, 129, 4112), (1, 5, 131072), (7, 64, 2048),
+          (8, 4096, 4096), (5, 333, 4112), (6, 1, 131072), (8, 7, 16), (9, 70, 2048)]
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in SHAPES])
@@ -158,7 +159,7 @@ def test_surface_matmul_int8_forms(oracle):
         linalg.matmul_int8((qa, ea[:44]), b)
 
 
-@pytest.mark.parametrize("shape", [(1, 4096, 4096), (200, 300, 4097), (8, 300, 1000)])
+@pytest.mark.parametrize("shape", [(1, 4096, 4096), (200, 300, 4097), (8, 300, 1000), (8, 300, 1024)])
 def test_gemm_int8i32_ws_in_graph(oracle, shape):
     """The caller-workspace entry (split-k partials, repack) captured in a HIP graph and
     replayed three times, eager work between replays; every replay bit-identical."""
