@@ -23,6 +23,7 @@ struct GemmProblem {
   int64_t ldc;           // C row stride in elements; 0 = n
   int seed;              // one leaf only: each chain starts from the flushed old C, not +0
   int seq;               // the caller's word (strides, seed): always the tile kernel
+  int whole;             // one column range: never split into whole rounds + a grouped tail
 };
 
 // Workspace floats run_gemm needs for `p` (0 when the product folds in one launch).

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "contract.h"
 #include "device_common.h"
 #include "gemv.h"
@@ -84,11 +86,56 @@ static int64_t repack_floats(const GemmProblem& p, bool is_a) {
 
 static int64_t round_floats(int64_t f) { return (f + 63) / 64 * 64; }
 
+// A tile product whose tiles fill whole rounds of the CUs and leave a short last round (the LM
+// head: 4 x 393 tiles on 256 CUs is 6 rounds and 36 tiles) runs as two column ranges: the
+// columns of the whole rounds as they are (p1), and the remaining columns (p2) with their leaves
+// split into aligned groups, so the last round is many short workgroups folded afterwards in the
+// contract's order.  A cell's leaves and tree are the same in either range: the bits are the
+// unsplit product's.  Only for operands loaded in place, one group per tile in the unsplit
+// product, and a grouped tail of at most half a round's time.
+static bool tail_split(const GemmProblem& p, int64_t P, int num_cus, GemmProblem& p1, GemmProblem& p2) {
+  if (p.whole || p.seq || p.seed || P < 2 || num_cus <= 0) return false;
+  const int64_t tm = (p.m + BM - 1) / BM, tn = (p.n + BN - 1) / BN, T = tm * tn;
+  if (T <= num_cus || pick_group(P, T, num_cus) < P) return false;
+  if (!in_place(p, true) || !in_place(p, false)) return false;
+  const int64_t tn1 = T / num_cus * num_cus / tm;  // column tiles of the whole rounds
+  if (tn1 < 1 || tn1 >= tn) return false;
+  const int64_t r = tm * (tn - tn1);  // tail tiles
+  const int64_t gsz = pick_group(P, r, num_cus);
+  const int64_t ng = (P + gsz - 1) / gsz;
+  if (ng < 2 || 2 * ((r * ng + num_cus - 1) / num_cus) > ng) return false;  // tail <= half a round
+  const int64_t n1 = tn1 * BN;
+  int64_t rows, cols, a_rs, a_cs, b_rs, b_cs;
+  stored_shape(p, true, rows, cols);
+  stored_strides(p, true, cols, a_rs, a_cs);
+  stored_shape(p, false, rows, cols);
+  stored_strides(p, false, cols, b_rs, b_cs);
+  p1 = p;
+  p1.whole = 1;
+  p1.strided = 1;
+  p1.a_rs = a_rs; p1.a_cs = a_cs; p1.b_rs = b_rs; p1.b_cs = b_cs;
+  p1.ldc = p.ldc > 0 ? p.ldc : p.n;
+  p2 = p1;
+  p1.n = n1;
+  p2.n = p.n - n1;
+  if (p.c) p2.c = p.c + n1;  // (sizing queries pass no operands)
+  // B's columns n1.. : later columns of each stored row (NN, TN) or later stored rows (NT)
+  const int64_t boff = p.op == OP_NT ? n1 * b_rs : n1 * b_cs;
+  if (p.b) p2.b = static_cast<const char*>(p.b) + boff * elem_bytes(p.b_type);
+  else if (boff * elem_bytes(p.b_type) % 16 != 0) return false;
+  if (p.scales) p2.scales = p.scales + n1;
+  if (p.bias) p2.bias = p.bias + n1;
+  return in_place(p1, false) && in_place(p2, false);
+}
+
 int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus) {
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
   if (P < 1 || p.m <= 0 || p.n <= 0) return 0;
   if (use_gemv(p)) return gemv_groups(P) > 1 ? gemv_groups(P) * p.m * p.n : 0;
+  GemmProblem p1, p2;
+  if (tail_split(p, P, num_cus, p1, p2))
+    return std::max(gemm_workspace_floats(p1, num_cus), gemm_workspace_floats(p2, num_cus));
   const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
   const int64_t gsz = P > 1 ? pick_group(P, tiles, num_cus) : 1;
   const int64_t ng = (P + gsz - 1) / gsz;
@@ -142,6 +189,11 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
       return launch_gemv_mfma_nn(vm, static_cast<const float*>(p.a), p.b_type, mgrid, stream);
     }
     return launch_gemv_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, vec, dim3((unsigned)grid), stream);
+  }
+  GemmProblem p1, p2;
+  if (tail_split(p, P, num_cus, p1, p2)) {
+    hipError_t e = run_gemm(p1, ws, counters, num_cus, stream);
+    return e != hipSuccess ? e : run_gemm(p2, ws, counters, num_cus, stream);
   }
   GemmArgs g;
   g.c = p.c; g.a = p.a; g.b = p.b; g.scales = p.scales; g.bias = p.bias; g.ws = ws;

@@ -346,3 +346,44 @@ def test_plan_in_graph_replays(oracle, case):
         torch.cuda.synchronize()
         assert_bits(plan.out.cpu().numpy(), want, f"{case} replay {rep}")
         gpu_gemm(*_operands(rng, 33, 40, 300, 0, "normal"), 0)  # eager work between replays
+
+
+# Products whose tiles fill whole rounds of the CUs and leave a short last round run as two
+# column ranges, the tail with its leaves in aligned groups (on 256 CUs: 4 x 65 = 260 tiles, 64
+# column tiles whole, the last one grouped).  Every cell against the oracle, bias included.
+TAIL = [(0, "f32", 512, 8320, 512, True), (1, "f32", 512, 8300, 384, False), (2, "f32", 512, 8320, 256, True),
+        (0, "bf16", 512, 8320, 512, False), (1, "bf16", 512, 8300, 640, True), (0, "i8", 512, 8320, 512, True),
+        (1, "i8", 512, 8304, 512, False)]
+
+
+@pytest.mark.parametrize("case", TAIL, ids=[f"op{o}-{w}-{m}x{n}x{k}{'-bias' if b else ''}" for o, w, m, n, k, b in TAIL])
+def test_tail_split_vs_oracle(oracle, case):
+    op, wt, m, n, k, with_bias = case
+    D = _dev()
+    print(f"tail split {case}", flush=True)
+    rng = np.random.default_rng(m + n + k + op)
+    a, b = _operands(rng, m, n, k, op, "wide")
+    bias = _values(rng, (n,), "wide") if with_bias else None
+    ta = torch.from_numpy(a).to(DEV)
+    tbias = None if bias is None else torch.from_numpy(bias).to(DEV)
+    b_type = {"f32": 0, "bf16": 1, "i8": 2}[wt]
+    if wt == "f32":
+        want = oracle.gemm_fast(a, b, op)
+        c = D.gemm(ta, torch.from_numpy(b).to(DEV), op=op, bias=tbias)
+    elif wt == "bf16":
+        bb = oracle.bf16_narrow(b)
+        want = oracle.gemm_fast(a, oracle.bf16_widen(bb), op)
+        c = D.gemm_bf16w(ta, torch.from_numpy(bb.view(np.int16)).to(DEV), op=op, bias=tbias)
+    else:
+        codes = rng.integers(-127, 128, b.shape, dtype=np.int8)
+        scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        want = oracle.gemm_fast(a, oracle.int8_dequant(codes, scales, op), op)
+        c = D.gemm_int8w(ta, torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV), op=op,
+                         bias=tbias)
+    torch.cuda.synchronize()
+    if with_bias:
+        want = oracle.bias(want, bias)
+    assert_bits(c.cpu().numpy(), oracle.nan_canon(want), "tail split")
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        # the grouped tail's roots are the only workspace these in-place products need
+        assert D.workspace_bytes(m, n, k, op=op, b_type=b_type) > 0
