@@ -271,6 +271,39 @@ def bench_seq(torch, D, W, O, steps, warmup, check, runs=1):
     return out
 
 
+#: The reference's fp32.v1 and bf16f32.v1 rows on MI325X (INFERENCE, the median ms of one call and
+#: one synchronize per sample; the weights W[n][k] packed once, OP_NT;
+#: bench/results/lowbit_units/2026-09-29/TABLE.md:76-89).
+LLAMA_ROWS = [("qkv.t1", 1, 4096, 4096, 0.0617, 1.1249), ("qkv.t8", 8, 4096, 4096, 0.0775, 0.1078),
+              ("qkv.t512", 512, 4096, 4096, 0.9254, 0.9480), ("mlp_up.t1", 1, 14336, 4096, 0.1631, 1.1905),
+              ("mlp_up.t8", 8, 14336, 4096, 0.1677, 0.2920), ("mlp_up.t512", 512, 14336, 4096, 2.3895, 2.5044),
+              ("mlp_down.t1", 1, 4096, 14336, 0.1560, 3.9026), ("mlp_down.t8", 8, 4096, 14336, 0.1947, 0.3250),
+              ("mlp_down.t512", 512, 4096, 14336, 2.5107, 2.5862), ("lm_head.t1", 1, 128256, 4096, 1.3122, 2.5466),
+              ("lm_head.t8", 8, 128256, 4096, 1.2280, 2.4984), ("lm_head.t512", 512, 16032, 4096, 2.7776, 2.9081)]
+
+
+def bench_llama(torch, D, steps, warmup):
+    """The reference's Llama-8B projection rows, fp32 and bf16-stored weights (OP_NT, W[n][k]
+    resident, the same buffers every call), device time per product as graph replays; the
+    reference's times include one host synchronize per call.  Random weights, made on the device."""
+    out = {}
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(9)
+    for name, m, n, k, ref32, ref16 in LLAMA_ROWS:
+        x = torch.randn((m, k), generator=g, device="cuda:0")
+        w = torch.randn((n, k), generator=g, device="cuda:0") * 0.02
+        row = {}
+        for kind, wt, ref in (("fp32", w, ref32), ("bf16w", w.to(torch.bfloat16).view(torch.int16), ref16)):
+            plan = D.Plan(x, wt, op=D.OP_NT)
+            ms = graph_time([plan], max(3, steps // 2), max(3, warmup // 4), torch)
+            row[kind] = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "reference_mi325x_ms": ref,
+                         "speedup_vs_reference": ref / ms}
+            del plan
+        out[name] = row
+        del x, w
+    return out
+
+
 #: The reference's host budget for its scalar oracle arm, in multiply-accumulates
 #: (bench/gemm_card_main.mojo:241), and its rule for meeting it (:361-378): halve n (or m, when
 #: m > n) until m*n*k fits; k is never touched, so every cell keeps its leaves and tree.
@@ -586,6 +619,7 @@ def main():
         extra["compare"] = bench_compare(torch, D, args.steps, args.warmup)
         extra["int8i32"] = bench_int8i32(torch, O, args.steps, args.warmup, check)
         extra["int15i64"] = bench_int15i64(torch, O, args.steps, args.warmup, check)
+        extra["llama_fp32_bf16w"] = bench_llama(torch, D, args.steps, args.warmup)
 
     line = {
         "metric": "identical-mode FP32 GEMM TFLOP/s & % of peak; GEMV GB/s; 0 mismatched bits",
