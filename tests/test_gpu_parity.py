@@ -308,7 +308,7 @@ def test_skinny_m_nt(oracle, shape, wt):
     assert_bits(got.cpu().numpy(), oracle.nan_canon(want), f"skinny NT {wt} {shape}")
 
 
-@pytest.mark.parametrize("case", ["skinny_i8", "mfma_groups", "mfma_bias"])
+@pytest.mark.parametrize("case", ["skinny_i8", "mfma_groups", "mfma_bias", "mfma_tail_split"])
 def test_plan_in_graph_replays(oracle, case):
     """A Plan (caller workspace, no allocation per call) captured in a HIP graph: every replay,
     with eager products and synchronizations between replays, gives the oracle's bits."""
@@ -323,9 +323,11 @@ def test_plan_in_graph_replays(oracle, case):
                       scales=torch.from_numpy(scales).to(DEV))
         want = oracle.gemm_fast(a, oracle.int8_dequant(codes, scales, 0), 0)
     else:
-        m, n, k = 150, 170, 8192 if case == "mfma_groups" else 700
+        # the tail split: on 256 CUs, 64 column tiles whole and the last one in leaf groups
+        m, n, k = {"mfma_groups": (150, 170, 8192), "mfma_bias": (150, 170, 700),
+                   "mfma_tail_split": (512, 8320, 512)}[case]
         a, b = _operands(rng, m, n, k, 0, "wide")
-        bias = _values(rng, (n,), "wide") if case == "mfma_bias" else None
+        bias = _values(rng, (n,), "wide") if case in ("mfma_bias", "mfma_tail_split") else None
         plan = D.Plan(torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV),
                       bias=None if bias is None else torch.from_numpy(bias).to(DEV))
         want = oracle.gemm_fast(a, b, 0)
