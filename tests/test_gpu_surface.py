@@ -71,10 +71,12 @@ def _device_product(kind, a, b, op, extra=None):
 
 # (kind, m, n, k, op): A of 16 MB or more is cut into row bands of 256-row multiples
 # (2304 x 4096 f32: bands of 1280 + 1024; 3000 x 4096 NT: 1024 + 1024 + 952), OP_TN and
-# small products take one band
+# small products take one band; 512 x 8320 x 512 is 260 tiles, on 256 CUs the whole-rounds +
+# grouped-tail split inside the surface's own stream-ordered workspace
 BAND_CASES = [("f32", 2304, 640, 4096, 0), ("f32", 3000, 384, 4096, 1), ("f32", 640, 512, 8192, 2),
               ("bias", 2304, 520, 4096, 0), ("bf16", 4100, 256, 2048, 1), ("int8", 2500, 1000, 4096, 0),
-              ("f32", 37, 41, 300, 0)]
+              ("f32", 37, 41, 300, 0), ("f32", 512, 8320, 512, 0), ("bias", 512, 8320, 512, 0),
+              ("int8", 512, 8320, 512, 1)]
 
 
 @pytest.mark.parametrize("case", BAND_CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}x{c[3]}-op{c[4]}" for c in BAND_CASES])
