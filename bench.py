@@ -7,9 +7,10 @@ counted).  Beside it: the kernel's roofline fraction (FP32 matrix peak 157.3 TFL
 other workloads (--all: 512^3, decode GEMV with an int8 weight at M = 1/4/16 in GB/s, the bf16
 SwiGLU up projection, the adversarial LM head, and one GPU's N/8 column shard of the decode GEMV
 and of the prefill, each the median of 20 timed runs with the fastest and slowest), the
-mismatching words against the CPU oracle on sampled rows, and the CPU oracle timed on the host
-cores (with --all, both arms on every workload: the scalar oracle on one thread, the fast one
-on every thread, and the host's CPU).
+mismatching words against the CPU oracle over every output cell (the output first filled with a
+poison word), and the CPU baseline timed on the host cores: the scalar oracle on one thread on
+the reference's host-capped block (the headline `cpu_baseline`) and the reference's fast CPU
+column restated on every thread (with --all, both arms on every workload, and the host's CPU).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
 """
@@ -100,6 +101,9 @@ def profiled_traffic(path=PREFILL_PROFILE):
     return None
 
 
+POISON = -987654.0  # an output cell no kernel writes keeps it (gemm/checks/gemm_device_check.mojo:111)
+
+
 def _rows(m, count=8):
     if m <= count:
         return np.arange(m)
@@ -122,15 +126,20 @@ def bench_prefill(torch, D, W, O, steps, warmup, check, runs=1, cols=None):
         w, bias = np.ascontiguousarray(w[:, :cols]), np.ascontiguousarray(bias[:cols])
     plan = D.Plan(_t(torch, x), _t(torch, w), bias=_t(torch, bias))
     res = _timed([plan], steps, warmup, torch, runs)
+    res["out"] = None
     ms = res["ms"]
     m, k = x.shape
     n = w.shape[1]
     res["tflops"] = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     if check:
-        rows = _rows(m)
-        want = O.nan_canon(O.bias(O.gemm_fast(x[rows], w, 0), bias))
-        res["mismatched_words"] = _mismatch(plan.out.cpu().numpy()[rows], want)
-        res["checked_cells"] = int(rows.size * n)
+        # every cell, on an output first filled with the poison word
+        plan.out.fill_(POISON)
+        plan()
+        want = O.nan_canon(O.bias(O.gemm_fast(x, w, 0), bias))
+        got = plan.out.cpu().numpy()
+        res["mismatched_words"] = _mismatch(got, want)
+        res["checked_cells"] = int(m * n)
+        res["out"] = got
     return res
 
 
@@ -144,9 +153,10 @@ def bench_product(torch, D, a, b, steps, warmup, want_fn=None, runs=1):
     n = b.shape[1]
     res["tflops"] = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     if want_fn is not None:
-        rows = _rows(m)
-        res["mismatched_words"] = _mismatch(plan.out.cpu().numpy()[rows], want_fn(rows))
-        res["checked_cells"] = int(len(rows) * n)
+        plan.out.fill_(POISON)
+        plan()
+        res["mismatched_words"] = _mismatch(plan.out.cpu().numpy(), want_fn())
+        res["checked_cells"] = int(m * n)
     return res
 
 
@@ -172,6 +182,7 @@ def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=N
                 "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12, "bytes": nbytes})
     if check:
+        out.fill_(POISON)
         plans[0]()
         if wdeq is None:
             wdeq = O.int8_dequant(codes, scales, 0)
@@ -181,25 +192,48 @@ def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=N
     return res
 
 
-def cpu_baseline(W, O, min_seconds=10.0, max_seconds=30.0):
-    """The CPU oracle's fast arm (AVX2 FMA, every host thread) on the whole prefill product,
-    repeated until about `min_seconds` have passed; GFLOP/s of the same arithmetic."""
-    x, w, bias = W.prefill()
-    threads = O.max_threads()
+def _repeat(fn, min_seconds, max_seconds):
+    """Call fn until about `min_seconds` have passed; (calls, seconds, last result)."""
     reps, t0 = 0, time.perf_counter()
     while True:
-        y = O.gemm_fast(x, w, 0, threads=threads)
-        O.bias(y, bias)
+        y = fn()
         reps += 1
         dt = time.perf_counter() - t0
         if dt >= min_seconds or dt * (reps + 1) / reps > max_seconds:
-            break
+            return reps, dt, y
+
+
+def cpu_baseline(W, O, gpu_out=None, min_seconds=10.0, max_seconds=30.0):
+    """Both CPU arms on the prefill projection, timed on this host.
+
+    Arm (i), the headline: the scalar oracle (orc_gemm: the reference CPU binding's algorithm,
+    decomposition/linalg_host_impl.mojo:39-47 -> gemm/host/gemm_oracle.mojo:357-371) on ONE
+    thread, on the block the reference's host budget allows (16 M multiply-accumulates: m and n
+    halved, k untouched; bench/gemm_card_main.mojo:361-378), + bias, repeated for about
+    `min_seconds`; capped.  Its words are compared with the same block of the GPU's output.
+    Arm (ii): the reference's fast CPU column (orc_host_rows, gemm/host/gemm_host_rows.mojo,
+    deferred flush with redo) on every host thread, the whole product + bias."""
+    x, w, bias = W.prefill()
     m, k = x.shape
     n = w.shape[1]
-    return {"value": round(2.0 * m * n * k * reps / dt / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
+    mm, nn = host_capped(m, n, k)
+    xs, ws, bs = np.ascontiguousarray(x[:mm]), np.ascontiguousarray(w[:, :nn]), np.ascontiguousarray(bias[:nn])
+    reps, dt, y = _repeat(lambda: O.bias(O.gemm(xs, ws, 0), bs), min_seconds, max_seconds)
+    arm1 = {"value": round(2.0 * mm * nn * k * reps / dt / 1e9, 4), "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "capped": True,
+            "sample": f"the {mm}x{nn} block of the prefill product (X[:{mm}] . W[:, :{nn}], k = {k}, + bias: the "
+                      f"reference's 16M-MAC host cap) x {reps}, oracle/gemm_oracle.c orc_gemm (the scalar "
+                      f"gemm_oracle), 1 thread, {dt:.1f} s"}
+    if gpu_out is not None:
+        arm1["mismatched_words_vs_gpu"] = _mismatch(O.nan_canon(y), gpu_out[:mm, :nn])
+    threads = O.max_threads()
+    reps, dt, _ = _repeat(lambda: O.bias(O.host_rows(x, w, 0, threads=threads), bias), min_seconds, max_seconds)
+    arm2 = {"value": round(2.0 * m * n * k * reps / dt / 1e9, 3), "unit": "GFLOP/s", "cores": threads,
             "kind": "port",
-            "sample": f"the whole prefill product (X[2048x4096] . W[4096x4096] + bias) x {reps}, "
-                      f"oracle/gemm_oracle.c fast arm (AVX2 FMA), {threads} threads, {dt:.1f} s"}
+            "sample": f"the whole prefill product + bias x {reps}, oracle/gemm_oracle.c orc_host_rows (the "
+                      f"reference's gemm_host_rows: AVX2 FMA, deferred flush with redo), {threads} threads, "
+                      f"{dt:.1f} s"}
+    return arm1, arm2
 
 
 class _SeqLinear:
@@ -336,8 +370,9 @@ def host_info():
 def cpu_arms(W, O):
     """Both CPU arms on the five workloads, timed on this host: (i) the scalar oracle (the
     reference's CPU binding's algorithm) on one thread, full size for 512^3 and the decode GEMV,
-    capped by the reference's host budget for the three large products; (ii) the fast oracle
-    (AVX2 FMA) on every host thread, full size.  Where an arm ran a capped block, its bits are
+    capped by the reference's host budget for the three large products; (ii) the reference's fast
+    CPU column restated (orc_host_rows: AVX2 FMA, deferred flush with redo) on every host thread,
+    full size.  Where an arm ran a capped block, its bits are
     compared with the same block of the fast arm's full output (a cell's arithmetic depends on
     k only, so the block must match word for word)."""
     threads = O.max_threads()
@@ -353,12 +388,12 @@ def cpu_arms(W, O):
         m, k = a.shape
         n = b.shape[1]
         post = post or (lambda y, cols: y)
-        fast, rf = arm(lambda: post(O.gemm_fast(a, b, 0, threads=threads), n), m, n, k)
+        fast, rf = arm(lambda: post(O.host_rows(a, b, 0, threads=threads), n), m, n, k)
         mm, nn = (m, n) if full else host_capped(m, n, k)
         sa, sb = np.ascontiguousarray(a[:mm]), np.ascontiguousarray(b[:, :nn])
         scal, rs = arm(lambda: post(O.gemm(sa, sb, 0), nn), mm, nn, k)
         rs["capped"] = (mm, nn) != (m, n)
-        rs["mismatched_words_vs_fast"] = _mismatch(scal, fast[:mm, :nn])
+        rs["mismatched_words_vs_fast"] = _mismatch(O.nan_canon(scal), O.nan_canon(fast[:mm, :nn]))
         rows[name] = {"scalar_1_thread": rs, "fast_all_threads": rf}
 
     a, b = W.gemm512()
@@ -584,14 +619,16 @@ def main():
 
     check = not args.no_check
     pre = bench_prefill(torch, D, W, O, args.steps, args.warmup, check)
+    gpu_out = pre.pop("out")
     extra = {}
     if args.all:
         # every row: the median of RUNS timed runs (graph replays), with the fastest and slowest
         R = 20
         extra["prefill"] = bench_prefill(torch, D, W, O, args.steps, args.warmup, check, runs=R)
+        extra["prefill"].pop("out")
         a, b = W.gemm512()
         extra["gemm512"] = bench_product(torch, D, a, b, args.steps, args.warmup,
-                                         want_fn=(lambda r: O.gemm(a[r], b, 0)) if check else None, runs=R)
+                                         want_fn=(lambda: O.gemm(a, b, 0)) if check else None, runs=R)
         x16, codes, scales = W.decode()
         wdeq = O.int8_dequant(codes, scales, 0) if check else None
         del x16, codes, scales
@@ -601,17 +638,18 @@ def main():
         x, wb = W.swiglu_up()
         extra["swiglu_up"] = bench_product(
             torch, D, x, wb, max(3, args.steps // 4), max(3, args.warmup // 10),
-            want_fn=(lambda r: O.gemm_fast(x[r], O.bf16_widen(wb), 0)) if check else None, runs=R)
+            want_fn=(lambda: O.gemm_fast(x, O.bf16_widen(wb), 0)) if check else None, runs=R)
         x, w = W.lm_head()
         extra["lm_head"] = bench_product(
             torch, D, x, w, max(3, args.steps // 2), max(3, args.warmup // 4),
-            want_fn=(lambda r: O.nan_canon(O.gemm_fast(x[r], w, 0))) if check else None, runs=R)
+            want_fn=(lambda: O.nan_canon(O.gemm_fast(x, w, 0))) if check else None, runs=R)
         del x, w, wb
         # one GPU's share of the two products a column split spreads over 8 GPUs: N/8 columns
         extra["shard_decode_m1_n1792"] = bench_decode(torch, D, W, O, 1, args.steps, args.warmup, check,
                                                       runs=R, cols=14336 // 8, wdeq=wdeq)
         extra["shard_prefill_n512"] = bench_prefill(torch, D, W, O, args.steps, args.warmup, check, runs=R,
                                                     cols=4096 // 8)
+        extra["shard_prefill_n512"].pop("out")
         del wdeq
         extra.update(bench_seq(torch, D, W, O, args.steps, args.warmup, check, runs=R))
 
@@ -653,7 +691,7 @@ def main():
     if extra:
         line["workloads"] = _round(extra)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(W, O)
+        line["cpu_baseline"], line["cpu_baseline_fast_column"] = cpu_baseline(W, O, gpu_out)
         if args.all:
             line["cpu_arms"] = _round(cpu_arms(W, O))
     print(json.dumps(line), flush=True)

@@ -94,19 +94,43 @@ int mlg_gemm_int8w(float* c, const float* a, const int8_t* codes, const float* s
                    void* stream);
 
 /* The general device entry with a caller-supplied workspace: it allocates no device memory
- * for the product (so a caller may capture it in a HIP graph), apart from a per-(device,
- * stream) buffer of completion counters created zeroed on the first call on that stream.
+ * and never synchronizes (so a caller may capture it in a HIP graph).
  * a_type: 0 float32, 1 bf16 bits; b_type: 0 float32, 1 bf16 bits, 2 int8 codes (with
- * `scales`, one per output column).  `workspace` must hold mlg_gemm_workspace_bytes() bytes
- * (0 bytes for most shapes; NULL is then accepted).  Calls sharing one workspace must be
- * ordered (one stream).  Same semantics as mlg_gemm_f32/bf16w/int8w otherwise. */
+ * `scales`, one per output column).  `workspace` must hold mlg_gemm_workspace_bytes_for()
+ * bytes (0 bytes for most shapes; NULL is then accepted).  Its first mlg_gemm_counter_bytes()
+ * bytes are completion counters: zero them before the workspace's first product; every
+ * product leaves them zero, so a workspace that serves one product shape needs no clearing
+ * between calls (a workspace that served another shape must be zeroed again).  Calls sharing
+ * one workspace must be ordered (one stream).  Same semantics as mlg_gemm_f32/bf16w/int8w
+ * otherwise.  (The reference's GemmWorkspace.run, gemm/checks/gemm_identical.mojo:10712-10888.) */
 int mlg_gemm_ws(float* c, const void* a, const void* b, const float* scales, const float* bias,
                 int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type,
                 int64_t leaf, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Bytes of workspace mlg_gemm_ws needs for this product on the current device (-1 on error). */
+/* Bytes of workspace mlg_gemm_ws needs for this product on the current device, for operands
+ * a, b at these addresses (an operand the tile kernel cannot load in place -- base not 16-byte
+ * aligned, rows not a multiple of 16 bytes -- is repacked into the workspace); -1 on error.
+ * (identical_gemm_workspace_max_floats, gemm/checks/gemm_identical.mojo:10789-10844.) */
+int64_t mlg_gemm_workspace_bytes_for(const void* a, const void* b, int64_t m, int64_t n, int64_t k, int32_t op,
+                                     int32_t a_type, int32_t b_type, int64_t leaf);
+
+/* The same for operands that are 16-byte aligned with rows of a multiple of 16 bytes. */
 int64_t mlg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type,
                                  int32_t b_type, int64_t leaf);
+
+/* Bytes of completion counters at the start of that workspace (0 for most products). */
+int64_t mlg_gemm_counter_bytes(int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type,
+                               int64_t leaf);
+
+/* Which kernels this product dispatches to, as bits (nothing launched, no operand read;
+ * num_cus 0 = the current device's count, > 0 = that count, no device needed):
+ *   1 gemm_mfma_kernel  2 fold_groups_kernel after it  4 gemv_nn_kernel  8 gemv_nt_kernel
+ *   16 gemv_mfma4_nn_kernel  32 gemv_mfma_nn_kernel  64 whole rounds + grouped tail
+ *   128 repack first  256 k = 0 (+0 stored)  512 a tile folds several leaves itself
+ *   1024 a skinny product folded across workgroups.
+ * -1 on error.  (The role of the reference's choose_gemm_plan, gemm_identical.mojo:4604-4801.) */
+int64_t mlg_gemm_route(const void* a, const void* b, int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type,
+                       int32_t b_type, int64_t leaf, int32_t num_cus);
 
 /*
  * The caller-partition and sequence-executor words on strided operand views (device pointers,

@@ -55,6 +55,12 @@ def lib():
         L.mlg_gemm_ws.restype = ctypes.c_int
         L.mlg_gemm_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i32, i64]
         L.mlg_gemm_workspace_bytes.restype = i64
+        L.mlg_gemm_workspace_bytes_for.argtypes = [vp, vp, i64, i64, i64, i32, i32, i32, i64]
+        L.mlg_gemm_workspace_bytes_for.restype = i64
+        L.mlg_gemm_counter_bytes.argtypes = [i64, i64, i64, i32, i32, i32, i64]
+        L.mlg_gemm_counter_bytes.restype = i64
+        L.mlg_gemm_route.argtypes = [vp, vp, i64, i64, i64, i32, i32, i32, i64, i32]
+        L.mlg_gemm_route.restype = i64
         L.mlg_gemm_leaf_ptr.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp]
         L.mlg_gemm_leaf_ptr.restype = ctypes.c_int
         L.mlg_gemm_leaf_ptr_epi.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, i32, vp, i32, vp]

@@ -56,54 +56,28 @@ int num_cus_of_current_device() {
   return cache[dev];
 }
 
-// Completion counters of the skinny-M path: one zeroed buffer per (device, stream), grown
-// on demand.  Products on one stream run in order and every product leaves its counters
-// at zero, so the buffer is never shared by two products in flight.
-unsigned int* stream_counters(hipStream_t stream, int64_t count) {
-  struct Entry { int dev; hipStream_t stream; unsigned int* ptr; int64_t cap; };
-  static std::mutex mu;
-  static std::vector<Entry> table;
-  int dev = 0;
-  hip_check(hipGetDevice(&dev), "hipGetDevice");
-  std::lock_guard<std::mutex> lock(mu);
-  for (Entry& e : table) {
-    if (e.dev == dev && e.stream == stream) {
-      if (e.cap >= count) return e.ptr;
-      // grow: wait for the stream (its products may still use the old buffer)
-      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
-      hip_check(hipFree(e.ptr), "hipFree");
-      e.ptr = nullptr;
-      e.cap = 0;
-      const int64_t cap = count < 4096 ? 4096 : count;
-      hip_check(hipMalloc((void**)&e.ptr, (size_t)cap * sizeof(unsigned int)), "hipMalloc");
-      hip_check(hipMemset(e.ptr, 0, (size_t)cap * sizeof(unsigned int)), "hipMemset");
-      e.cap = cap;
-      return e.ptr;
-    }
-  }
-  Entry e{dev, stream, nullptr, count < 4096 ? 4096 : count};
-  hip_check(hipMalloc((void**)&e.ptr, (size_t)e.cap * sizeof(unsigned int)), "hipMalloc");
-  hip_check(hipMemset(e.ptr, 0, (size_t)e.cap * sizeof(unsigned int)), "hipMemset");
-  table.push_back(e);
-  return e.ptr;
-}
-
-// Enqueue one product on `stream`; the group-root workspace (if any) is allocated from
-// the stream-ordered pool and released on the same stream, so calls on different
-// streams never share it.
-void enqueue_gemm(const mlg::GemmProblem& p, hipStream_t stream, void* user_ws = nullptr,
-                  int64_t user_ws_bytes = -1) {
+void check_problem(const mlg::GemmProblem& p, int cus) {
   if (p.m < 0 || p.n < 0 || p.k < 0) throw Fail("mlgemm: m, n and k must be >= 0");
   if (p.op != mlg::OP_NN && p.op != mlg::OP_NT && p.op != mlg::OP_TN)
     throw Fail("mlgemm: op must be 0 (OP_NN), 1 (OP_NT) or 2 (OP_TN), got " + std::to_string(p.op));
   if (p.leaf < 0) throw Fail("mlgemm: leaf must be >= 0 (0 = the contract's leaf size)");
+  // the reference refuses partitions beyond its kernels' fold stack the same way
+  // (gemm/neural_dispatch.mojo:284-285)
+  const std::string why = mlg::launch_limit(p, cus);
+  if (!why.empty()) throw Fail("mlgemm: " + why);
+}
+
+// Enqueue one product on `stream`.  Workspace: the caller's (user_ws_bytes >= 0; its counters
+// zero, as every product leaves them), or one allocated from the stream-ordered pool, its
+// counters zeroed by a kernel, and released on the same stream.
+void enqueue_gemm(const mlg::GemmProblem& p, hipStream_t stream, void* user_ws = nullptr,
+                  int64_t user_ws_bytes = -1) {
+  const int cus = num_cus_of_current_device();
+  check_problem(p, cus);
   if (p.m == 0 || p.n == 0) return;
   if (!p.c || (p.k > 0 && (!p.a || !p.b))) throw Fail("mlgemm: null operand pointer");
   if (p.b_type == mlg::T_I8 && p.k > 0 && !p.scales) throw Fail("mlgemm: int8 weight needs scales");
-  const int cus = num_cus_of_current_device();
   const int64_t wsf = mlg::gemm_workspace_floats(p, cus);
-  const int64_t ncnt = mlg::gemm_counter_count(p);
-  unsigned int* counters = ncnt > 0 ? stream_counters(stream, ncnt) : nullptr;
   float* ws = nullptr;
   const bool own_ws = user_ws_bytes < 0;
   if (!own_ws && wsf > 0) {
@@ -112,8 +86,12 @@ void enqueue_gemm(const mlg::GemmProblem& p, hipStream_t stream, void* user_ws =
                  std::to_string(wsf * (int64_t)sizeof(float)) + " this product needs (mlg_gemm_workspace_bytes)");
     ws = (float*)user_ws;
   }
-  if (own_ws && wsf > 0) hip_check(hipMallocAsync((void**)&ws, (size_t)wsf * sizeof(float), stream), "hipMallocAsync");
-  hipError_t e = mlg::run_gemm(p, ws, counters, cus, stream);
+  hipError_t e = hipSuccess;
+  if (own_ws && wsf > 0) {
+    hip_check(hipMallocAsync((void**)&ws, (size_t)wsf * sizeof(float), stream), "hipMallocAsync");
+    e = mlg::run_zero_words(reinterpret_cast<unsigned int*>(ws), mlg::gemm_counter_count(p), stream);
+  }
+  if (e == hipSuccess) e = mlg::run_gemm(p, ws, cus, stream);
   if (own_ws && ws) {
     hipError_t f = hipFreeAsync(ws, stream);
     if (e == hipSuccess) e = f;
@@ -706,11 +684,40 @@ int mlg_follow(float* c, int64_t ldc, int64_t m, int64_t n, int32_t epi, const f
 
 int64_t mlg_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type,
                                  int32_t b_type, int64_t leaf) {
+  return mlg_gemm_workspace_bytes_for(nullptr, nullptr, m, n, k, op, a_type, b_type, leaf);
+}
+
+int64_t mlg_gemm_workspace_bytes_for(const void* a, const void* b, int64_t m, int64_t n, int64_t k, int32_t op,
+                                     int32_t a_type, int32_t b_type, int64_t leaf) {
   int64_t out = -1;
   guarded([&] {
     mlg::GemmProblem p{};
-    p.m = m; p.n = n; p.k = k; p.op = op; p.a_type = a_type; p.b_type = b_type; p.leaf = leaf;
-    out = mlg::gemm_workspace_floats(p, num_cus_of_current_device()) * (int64_t)sizeof(float);
+    p.a = a; p.b = b; p.m = m; p.n = n; p.k = k; p.op = op; p.a_type = a_type; p.b_type = b_type; p.leaf = leaf;
+    const int cus = num_cus_of_current_device();
+    check_problem(p, cus);
+    out = mlg::gemm_workspace_floats(p, cus) * (int64_t)sizeof(float);
+  });
+  return out;
+}
+
+int64_t mlg_gemm_counter_bytes(int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type,
+                               int64_t leaf) {
+  mlg::GemmProblem p{};
+  p.m = m; p.n = n; p.k = k; p.op = op; p.a_type = a_type; p.b_type = b_type; p.leaf = leaf;
+  return mlg::gemm_counter_count(p) * (int64_t)sizeof(unsigned int);
+}
+
+int64_t mlg_gemm_route(const void* a, const void* b, int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type,
+                       int32_t b_type, int64_t leaf, int32_t num_cus) {
+  int64_t out = -1;
+  guarded([&] {
+    mlg::GemmProblem p{};
+    p.a = a; p.b = b; p.m = m; p.n = n; p.k = k; p.op = op; p.a_type = a_type; p.b_type = b_type; p.leaf = leaf;
+    const int cus = num_cus > 0 ? num_cus : num_cus_of_current_device();
+    check_problem(p, cus);
+    unsigned route = 0;
+    mlg::run_gemm(p, nullptr, cus, nullptr, &route);
+    out = route;
   });
   return out;
 }

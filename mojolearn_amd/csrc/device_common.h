@@ -63,16 +63,18 @@ constexpr int RSRC_WORD3 = 0x00020000;
 
 // Upper tree levels: fold `ngroups` group roots per cell (a subtree per aligned group,
 // so the rest of the contract's tree is the same rule applied to the roots).
-// The same rule for up to 1024 scalar partials (ten levels), slots named.
+// The same rule for up to 2^20 scalar partials (twenty levels), slots named.
 struct StackF {
-  float s0, s1, s2, s3, s4, s5, s6, s7, s8, s9;
+  float s0, s1, s2, s3, s4, s5, s6, s7, s8, s9, s10, s11, s12, s13, s14, s15, s16, s17, s18, s19;
 #define MLG_PUSH_LEVEL(L)                      \
   if (!((t >> L) & 1)) { s##L = x; return; } \
   x = s##L + x;
   __device__ __forceinline__ void push(float x, int t) {
     MLG_PUSH_LEVEL(0) MLG_PUSH_LEVEL(1) MLG_PUSH_LEVEL(2) MLG_PUSH_LEVEL(3) MLG_PUSH_LEVEL(4)
-    MLG_PUSH_LEVEL(5) MLG_PUSH_LEVEL(6) MLG_PUSH_LEVEL(7) MLG_PUSH_LEVEL(8)
-    s9 = x;
+    MLG_PUSH_LEVEL(5) MLG_PUSH_LEVEL(6) MLG_PUSH_LEVEL(7) MLG_PUSH_LEVEL(8) MLG_PUSH_LEVEL(9)
+    MLG_PUSH_LEVEL(10) MLG_PUSH_LEVEL(11) MLG_PUSH_LEVEL(12) MLG_PUSH_LEVEL(13) MLG_PUSH_LEVEL(14)
+    MLG_PUSH_LEVEL(15) MLG_PUSH_LEVEL(16) MLG_PUSH_LEVEL(17) MLG_PUSH_LEVEL(18)
+    s19 = x;
   }
 #undef MLG_PUSH_LEVEL
 #define MLG_ROOT_LEVEL(L) \
@@ -80,6 +82,8 @@ struct StackF {
   __device__ __forceinline__ float root(float x, int t) const {
     MLG_ROOT_LEVEL(0) MLG_ROOT_LEVEL(1) MLG_ROOT_LEVEL(2) MLG_ROOT_LEVEL(3) MLG_ROOT_LEVEL(4)
     MLG_ROOT_LEVEL(5) MLG_ROOT_LEVEL(6) MLG_ROOT_LEVEL(7) MLG_ROOT_LEVEL(8) MLG_ROOT_LEVEL(9)
+    MLG_ROOT_LEVEL(10) MLG_ROOT_LEVEL(11) MLG_ROOT_LEVEL(12) MLG_ROOT_LEVEL(13) MLG_ROOT_LEVEL(14)
+    MLG_ROOT_LEVEL(15) MLG_ROOT_LEVEL(16) MLG_ROOT_LEVEL(17) MLG_ROOT_LEVEL(18) MLG_ROOT_LEVEL(19)
     return x;
   }
 #undef MLG_ROOT_LEVEL

@@ -373,13 +373,16 @@ __device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[LEAVE
   }
   if (g.ngroups == 1) return;
 
-  // Count this group's roots in; the workgroup that completes the count folds.  The roots
-  // are device-coherent stores, complete (vmcnt) before the count is published.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  // Count this group's roots in; the workgroup that completes the count folds.  The barrier
+  // orders every thread's root stores before thread 0's count; the count is a release at
+  // agent scope (the roots are visible to every workgroup of the device before it is), and the
+  // workgroup that completes it takes an acquire fence at agent scope (every other group's
+  // roots are visible to it; the barrier after it hands that on to its other threads).
   __syncthreads();
   if (tid == 0) {
-    const unsigned int prev = __hip_atomic_fetch_add(&g.counter[cg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned int prev = __hip_atomic_fetch_add(&g.counter[cg], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev + 1 == (unsigned int)g.ngroups ? 1u : 0u;
+    if (last_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!last_flag) return;

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace mlg {
 
 // One product C = op(A) . op(B) under fp32.v1 on device buffers.
@@ -26,17 +28,42 @@ struct GemmProblem {
   int whole;             // one column range: never split into whole rounds + a grouped tail
 };
 
-// Workspace floats run_gemm needs for `p` (0 when the product folds in one launch).
+// Workspace floats run_gemm needs for `p`: [completion counters][group roots][A repacked]
+// [B repacked], each part 256-byte aligned (0 when the product folds in one launch and loads
+// its operands in place).
 int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus);
 
-// Completion counters the product needs (0 or one per 256-column block of the skinny-M
-// path); they must be zero on entry and are zero again when the product completes.
+// Completion counters at the start of that workspace (0, or one per column group of a skinny
+// product folded across workgroups).  They must be zero on entry; the product leaves them
+// zero again when it completes.
 int64_t gemm_counter_count(const GemmProblem& p);
 
-// Enqueue the product on `stream`.  `ws` must hold gemm_workspace_floats() floats and
-// `counters` gemm_counter_count() zeroed counters.  Returns hipSuccess or the launch error.
-hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int num_cus,
-                    hipStream_t stream);
+// Why the product cannot be launched, or "" if it can: the fold stack covers STACK_ROOTS
+// leaf-group roots per cell, a tile grid holds TILE_GROUPS leaf groups (blockIdx.y).
+std::string launch_limit(const GemmProblem& p, int num_cus);
+constexpr int64_t STACK_ROOTS = int64_t(1) << 20;
+constexpr int64_t TILE_GROUPS = 65535;
+
+// Kernels a product dispatches to (run_gemm with `route`: bits set, nothing launched).
+constexpr unsigned ROUTE_TILE = 1;          // gemm_mfma_kernel
+constexpr unsigned ROUTE_FOLD = 2;          // fold_groups_kernel after it (leaves in several groups)
+constexpr unsigned ROUTE_GEMV_NN = 4;       // gemv_nn_kernel
+constexpr unsigned ROUTE_GEMV_NT = 8;       // gemv_nt_kernel
+constexpr unsigned ROUTE_MFMA4 = 16;        // gemv_mfma4_nn_kernel
+constexpr unsigned ROUTE_MFMA16 = 32;       // gemv_mfma_nn_kernel
+constexpr unsigned ROUTE_TAIL_SPLIT = 64;   // two column ranges (whole rounds + grouped tail)
+constexpr unsigned ROUTE_REPACK = 128;      // repack_rows_kernel first
+constexpr unsigned ROUTE_ZERO_K = 256;      // k = 0: +0 stored
+constexpr unsigned ROUTE_TILE_STACK = 512;  // a tile folds several leaves in its own stack
+constexpr unsigned ROUTE_GEMV_GROUPS = 1024;  // a skinny product folded across workgroups
+
+// Enqueue the product on `stream`.  `ws` must hold gemm_workspace_floats() floats, its
+// counters zero.  With `route`, only report the kernels (no launch, no operand read).
+// Returns hipSuccess or the launch error.
+hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t stream, unsigned* route = nullptr);
+
+// Zero `count` words on `stream` with a kernel.
+hipError_t run_zero_words(unsigned int* p, int64_t count, hipStream_t stream);
 
 // Elementwise conversions used by the low-bit surface (to_bf16 / from_bf16).
 hipError_t run_bf16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream);

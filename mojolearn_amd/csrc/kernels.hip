@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <string>
 
 #include "contract.h"
 #include "device_common.h"
@@ -128,11 +129,51 @@ static bool tail_split(const GemmProblem& p, int64_t P, int num_cus, GemmProblem
   return in_place(p1, false) && in_place(p2, false);
 }
 
+// Why a product cannot be launched ("" if it can): the fold stack's reach (StackF: the skinny
+// kernels' cross-workgroup fold and fold_groups_kernel) and the grid's dimensions.
+std::string launch_limit(const GemmProblem& p, int num_cus) {
+  const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
+  const int64_t P = leaf_count(p.k, L);
+  if (P < 1 || p.m <= 0 || p.n <= 0) return "";
+  if (use_gemv(p)) {
+    const int64_t groups = gemv_groups(P);
+    const int64_t ncg = (p.n + gemv_cols(p.b_type, p.op) - 1) / gemv_cols(p.b_type, p.op);
+    if (groups > STACK_ROOTS)
+      return "more leaf-group roots (" + std::to_string(groups) + ") than the fold stack covers (" +
+             std::to_string(STACK_ROOTS) + "); use a larger leaf";
+    if (ncg * groups > INT32_MAX) return "more workgroups than one launch holds; use a larger leaf";
+    return "";
+  }
+  GemmProblem p1, p2;
+  if (tail_split(p, P, num_cus, p1, p2)) {
+    const std::string a = launch_limit(p1, num_cus);
+    return a.empty() ? launch_limit(p2, num_cus) : a;
+  }
+  const int64_t tiles = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
+  const int64_t gsz = P > 1 ? pick_group(P, tiles, num_cus) : 1;
+  const int64_t ng = (P + gsz - 1) / gsz;
+  if (ng > TILE_GROUPS)
+    return "more leaf groups (" + std::to_string(ng) + ") than a grid column holds (" + std::to_string(TILE_GROUPS) +
+           "); use a larger leaf";
+  if (tiles > INT32_MAX) return "more tiles than one launch holds";
+  return "";
+}
+
+int64_t gemm_counter_count(const GemmProblem& p) {
+  const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
+  const int64_t P = leaf_count(p.k, L);
+  if (!use_gemv(p) || p.m <= 0 || p.n <= 0 || gemv_groups(P) <= 1) return 0;
+  return (p.n + gemv_cols(p.b_type, p.op) - 1) / gemv_cols(p.b_type, p.op);
+}
+
+// Workspace: [completion counters][group roots][A repacked][B repacked], each part 256-byte
+// aligned; the counters only for a skinny product folded across workgroups.
 int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus) {
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
   if (P < 1 || p.m <= 0 || p.n <= 0) return 0;
-  if (use_gemv(p)) return gemv_groups(P) > 1 ? gemv_groups(P) * p.m * p.n : 0;
+  if (use_gemv(p))
+    return gemv_groups(P) > 1 ? round_floats(gemm_counter_count(p)) + gemv_groups(P) * p.m * p.n : 0;
   GemmProblem p1, p2;
   if (tail_split(p, P, num_cus, p1, p2))
     return std::max(gemm_workspace_floats(p1, num_cus), gemm_workspace_floats(p2, num_cus));
@@ -142,28 +183,24 @@ int64_t gemm_workspace_floats(const GemmProblem& p, int num_cus) {
   return (ng > 1 ? round_floats(ng * p.m * p.n) : 0) + repack_floats(p, true) + repack_floats(p, false);
 }
 
-int64_t gemm_counter_count(const GemmProblem& p) {
-  const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
-  const int64_t P = leaf_count(p.k, L);
-  if (!use_gemv(p) || p.n <= 0 || gemv_groups(P) <= 1) return 0;
-  return (p.n + gemv_cols(p.b_type, p.op) - 1) / gemv_cols(p.b_type, p.op);
-}
-
-hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int num_cus,
-                    hipStream_t stream) {
+hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t stream, unsigned* route) {
   if (p.m <= 0 || p.n <= 0) return hipSuccess;
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
   const int64_t ldc = p.ldc > 0 ? p.ldc : p.n;
-  if (P == 0) return launch_fold_groups(p.c, ldc, nullptr, p.bias, p.m, p.n, 0, stream);
+  if (P == 0) {
+    if (route) { *route |= ROUTE_ZERO_K; return hipSuccess; }
+    return launch_fold_groups(p.c, ldc, nullptr, p.bias, p.m, p.n, 0, stream);
+  }
   if (use_gemv(p)) {
     GemvArgs v;
     v.c = p.c; v.w = p.b; v.scales = p.scales; v.bias = p.bias;
-    v.ws = ws; v.counter = counters;
     v.m = p.m; v.n = p.n; v.k = p.k; v.leaf = L; v.nleaves = P;
     v.ngroups = gemv_groups(P);
     v.ncg = (p.n + gemv_cols(p.b_type, p.op) - 1) / gemv_cols(p.b_type, p.op);
-    if (v.ngroups > 1 && (ws == nullptr || counters == nullptr)) return hipErrorInvalidValue;
+    // workspace: the column groups' completion counters, then the group roots
+    v.counter = reinterpret_cast<unsigned int*>(ws);
+    v.ws = ws ? ws + round_floats(gemm_counter_count(p)) : nullptr;
     const int eb = elem_bytes(p.b_type);
     int vec;
     if (p.op == OP_NT) {
@@ -174,26 +211,34 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
       vec = ((p.n * eb) % 4 == 0) && aligned(p.b, 4) && (int64_t)GV_CH * p.n * eb < (int64_t(1) << 31) ? 1 : 0;
       if (vec && L == GV_CH && p.k % GV_CH == 0) vec = 2;
     }
-    const int64_t grid = v.ncg * v.ngroups;
-    if (p.op == OP_NT)
-      return launch_gemv_nt(v, static_cast<const float*>(p.a), p.b_type, p.m, vec - 3, dim3((unsigned)grid), stream);
-    if (vec == 2 && p.m >= GV_MFMA4_MIN_M && aligned(p.a, 16) && 16 * p.k * 4 < (int64_t(1) << 31)) {
-      // the matrix-core kernels: fewer, wider groups (at most the workspace and counters sized
-      // for gemv_groups)
-      GemvArgs vm = v;
-      const bool four = p.m <= GV_MFMA4_MAX_M;
-      const int leaves = four ? MF4_LEAVES : MF_LEAVES;
-      vm.ngroups = (P + leaves - 1) / leaves;
-      const dim3 mgrid((unsigned)(vm.ncg * vm.ngroups));
-      if (four) return launch_gemv_mfma4_nn(vm, static_cast<const float*>(p.a), p.b_type, p.m, mgrid, stream);
-      return launch_gemv_mfma_nn(vm, static_cast<const float*>(p.a), p.b_type, mgrid, stream);
+    const bool mfma = p.op == OP_NN && vec == 2 && p.m >= GV_MFMA4_MIN_M && aligned(p.a, 16) &&
+                      16 * p.k * 4 < (int64_t(1) << 31);
+    const bool four = p.m <= GV_MFMA4_MAX_M;
+    if (mfma) v.ngroups = (P + (four ? MF4_LEAVES : MF_LEAVES) - 1) / (four ? MF4_LEAVES : MF_LEAVES);
+    if (route) {
+      *route |= p.op == OP_NT ? ROUTE_GEMV_NT : (mfma ? (four ? ROUTE_MFMA4 : ROUTE_MFMA16) : ROUTE_GEMV_NN);
+      if (v.ngroups > 1) *route |= ROUTE_GEMV_GROUPS;
+      return hipSuccess;
     }
-    return launch_gemv_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, vec, dim3((unsigned)grid), stream);
+    if (gemv_groups(P) > 1 && ws == nullptr) return hipErrorInvalidValue;
+    if (p.op == OP_NT)
+      return launch_gemv_nt(v, static_cast<const float*>(p.a), p.b_type, p.m, vec - 3,
+                            dim3((unsigned)(v.ncg * v.ngroups)), stream);
+    if (mfma) {
+      // the matrix-core kernels: fewer, wider groups (at most the workspace sized for
+      // gemv_groups)
+      const dim3 mgrid((unsigned)(v.ncg * v.ngroups));
+      if (four) return launch_gemv_mfma4_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, mgrid, stream);
+      return launch_gemv_mfma_nn(v, static_cast<const float*>(p.a), p.b_type, mgrid, stream);
+    }
+    return launch_gemv_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, vec, dim3((unsigned)(v.ncg * v.ngroups)),
+                          stream);
   }
   GemmProblem p1, p2;
   if (tail_split(p, P, num_cus, p1, p2)) {
-    hipError_t e = run_gemm(p1, ws, counters, num_cus, stream);
-    return e != hipSuccess ? e : run_gemm(p2, ws, counters, num_cus, stream);
+    if (route) *route |= ROUTE_TAIL_SPLIT;
+    hipError_t e = run_gemm(p1, ws, num_cus, stream, route);
+    return e != hipSuccess ? e : run_gemm(p2, ws, num_cus, stream, route);
   }
   GemmArgs g;
   g.c = p.c; g.a = p.a; g.b = p.b; g.scales = p.scales; g.bias = p.bias; g.ws = ws;
@@ -206,9 +251,16 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
   const int64_t gsz = P > 1 ? pick_group(P, tm * tn, num_cus) : 1;
   g.group = gsz;
   g.ngroups = (P + gsz - 1) / gsz;
+  const int64_t ra = repack_floats(p, true), rb = repack_floats(p, false);
+  if (route) {
+    *route |= ROUTE_TILE;
+    if (gsz > 1) *route |= ROUTE_TILE_STACK;
+    if (g.ngroups > 1) *route |= ROUTE_FOLD;
+    if (ra > 0 || rb > 0) *route |= ROUTE_REPACK;
+    return hipSuccess;
+  }
   // workspace: [group roots][A repacked][B repacked], each part 256-byte aligned
   float* wsp = ws + (g.ngroups > 1 ? round_floats(g.ngroups * p.m * p.n) : 0);
-  const int64_t ra = repack_floats(p, true), rb = repack_floats(p, false);
   if ((g.ngroups > 1 || ra > 0 || rb > 0) && ws == nullptr) return hipErrorInvalidValue;
   for (int which = 0; which < 2; ++which) {
     const bool is_a = which == 0;
@@ -239,6 +291,19 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, unsigned int* counters, int
   hipError_t e = launch_mfma(g, p.op, p.a_type, p.b_type, grid, stream);
   if (e != hipSuccess || g.ngroups == 1) return e;
   return launch_fold_groups(p.c, ldc, ws, p.bias, p.m, p.n, g.ngroups, stream);
+}
+
+// Zero `count` 32-bit words (the completion counters of a skinny product) with a kernel: a
+// memset node would not be safe in a captured graph.
+__global__ void zero_words_kernel(unsigned int* p, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) p[i] = 0u;
+}
+
+hipError_t run_zero_words(unsigned int* p, int64_t count, hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, p, count);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

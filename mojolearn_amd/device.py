@@ -224,17 +224,36 @@ def gemm_int15i64(ah, al, ea, bh, bl, eb, *, out=None):
 T_F32, T_BF16, T_I8 = 0, 1, 2
 
 
-def workspace_bytes(m, n, k, *, op=OP_NN, a_type=T_F32, b_type=T_F32, leaf=0):
-    """Workspace bytes `gemm_ws` needs for this product on the current device."""
-    nb = _native.lib().mlg_gemm_workspace_bytes(m, n, k, op, a_type, b_type, leaf)
+def workspace_bytes(m, n, k, *, op=OP_NN, a_type=T_F32, b_type=T_F32, leaf=0, a=None, b=None):
+    """Workspace bytes `gemm_ws` needs for this product on the current device (for the
+    operands `a`, `b` when given: a misaligned operand is repacked into the workspace)."""
+    pa = a.data_ptr() if a is not None else None
+    pb = b.data_ptr() if b is not None else None
+    nb = _native.lib().mlg_gemm_workspace_bytes_for(pa, pb, m, n, k, op, a_type, b_type, leaf)
     if nb < 0:
         _native.check(1)
     return nb
 
 
+#: Bits of `route` (include/mlgemm.h mlg_gemm_route).
+ROUTES = {"tile": 1, "fold": 2, "gemv_nn": 4, "gemv_nt": 8, "mfma4": 16, "mfma16": 32, "tail_split": 64,
+          "repack": 128, "zero_k": 256, "tile_stack": 512, "gemv_groups": 1024}
+
+
+def route(m, n, k, *, op=OP_NN, a_type=T_F32, b_type=T_F32, leaf=0, a=None, b=None, num_cus=0):
+    """The set of kernel names this product dispatches to (no launch).  With `num_cus` > 0 no
+    device is needed; `a`/`b` (tensors or integer addresses) decide the operands' alignment."""
+    addr = lambda t: None if t is None else (t if isinstance(t, int) else t.data_ptr())  # noqa: E731
+    r = _native.lib().mlg_gemm_route(addr(a), addr(b), m, n, k, op, a_type, b_type, leaf, num_cus)
+    if r < 0:
+        _native.check(1)
+    return {name for name, bit in ROUTES.items() if r & bit}
+
+
 class Plan:
-    """One product's arguments bound once (shapes checked, workspace allocated), so that a
-    call is a single C entry with no allocation -- capturable in a HIP graph.
+    """One product's arguments bound once (shapes checked, workspace allocated for these
+    operands and zeroed), so that a call is a single C entry with no allocation and no
+    synchronization -- capturable in a HIP graph.
 
     a: float32 (or bf16 bits with b_type=T_BF16), b: float32 / bf16 bits / int8 codes.
     """
@@ -251,8 +270,9 @@ class Plan:
             if scales.numel() != n:
                 raise ValueError(f"scales must hold n={n} values")
         self.out = _prep_out(out, m, n, a)
-        nb = workspace_bytes(m, n, k, op=op, a_type=a_type, b_type=b_type, leaf=leaf)
-        self.ws = torch.empty(max(nb, 4), dtype=torch.uint8, device=a.device)
+        nb = workspace_bytes(m, n, k, op=op, a_type=a_type, b_type=b_type, leaf=leaf, a=a, b=b)
+        # zeroed once: its completion counters start at zero and every call leaves them so
+        self.ws = torch.zeros(max(nb, 4), dtype=torch.uint8, device=a.device)
         self.args = (self.out.data_ptr(), a.data_ptr(), b.data_ptr(),
                      scales.data_ptr() if scales is not None else None, _bias(bias, n), m, n, k, op, a_type, b_type,
                      leaf, self.ws.data_ptr(), nb)

@@ -34,6 +34,34 @@
  * host-capped oracle card), the verify-table gemm cells, the closed-form fixtures F1-F8
  * of gemm/checks/gemm_oracle_check.mojo, exact-rational brute force on tiny shapes,
  * and literal-tree == register-stack fold for P = 1..2100.
+ *
+ * orc_host_rows restates the reference's fast CPU column itself
+ * (gemm/host/gemm_host_rows.mojo:163-225,246-556): flushed packed operands, panels of 32
+ * columns, the per-step flush DEFERRED with a subnormal tracker and the panel recomputed with
+ * a flush at every step when any raw result was subnormal, the fold in place, an unpacked
+ * per-step-flush path for m <= 4.
+ *
+ * PLANTED MISTAKES.  A build with -DORC_SABOTAGE=<n> (oracle/Makefile target `sabotage`,
+ * outputs under oracle/_sabotage/) plants one mistake of a plausible kind, so that a test can
+ * be shown able to fail: a GPU parity case whose oracle answer moves under a variant is a case
+ * that catches the same mistake in a kernel (tests/test_sabotage.py).  The default build
+ * (ORC_SABOTAGE 0) plants nothing.  Under any variant the fast arms return orc_gemm's answer,
+ * so the mistake reaches every caller (as the reference's GEMM_ORACLE_HOST_SABOTAGE does,
+ * gemm/host/gemm_host_rows.mojo:473-487).
+ *    1 fold pairs (q, q + width/2) instead of adjacent pairs (2q, 2q + 1)
+ *    2 an odd level's last partial added to +0 instead of carried
+ *    3 partials summed left to right (a serial fold)
+ *    4 a step as a multiply and then an add (two roundings) instead of one fma
+ *    5 a step whose exact value lies below 2^-126 flushed BEFORE rounding
+ *    6 operands entering a step unflushed
+ *    7 leaves of 32 steps (a tile kernel's slice) instead of the contract's leaf size
+ *    8 every leaf's chain started from -0.0
+ *    9 NaN words left with their payloads
+ *   10 the bias add without flushing its operands
+ *   11 the int8 column scale used unflushed
+ *   12 the accumulator not flushed between steps
+ *   13 orc_host_rows without the redo of its deferred flush (its own negative control,
+ *      gemm/host/gemm_host_rows.mojo:84-87,200-201)
  */
 #include <immintrin.h>
 #include <math.h>
@@ -47,6 +75,10 @@
 #define OP_NN 0
 #define OP_NT 1
 #define OP_TN 2
+
+#ifndef ORC_SABOTAGE
+#define ORC_SABOTAGE 0
+#endif
 
 static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
 static inline float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
@@ -64,6 +96,9 @@ float orc_fma(float a, float b, float c) { return fmaf(a, b, c); }
 /* gemm/contract.mojo:173-214 */
 int64_t orc_leaf_size(int64_t k) {
   if (k <= 0) return 1;
+#if ORC_SABOTAGE == 7
+  if (k > 32) return 32;
+#endif
   if (k <= K_LEAF_MIN) return k;
   int64_t p0 = (k + K_LEAF_MIN - 1) / K_LEAF_MIN;
   if (p0 <= MAX_LEAVES) return K_LEAF_MIN;
@@ -86,11 +121,34 @@ static inline float b_at(const float* b, int op, int64_t p, int64_t j, int64_t n
 }
 
 /* gemm/host/gemm_oracle.mojo:146-206 */
+static inline float chain_step(float a, float b, float acc) {
+#if ORC_SABOTAGE == 6
+  const float fa = a, fb = b;
+#else
+  const float fa = ftz(a), fb = ftz(b);
+#endif
+#if ORC_SABOTAGE == 4
+  const float prod = fa * fb; /* -ffp-contract=off: two roundings */
+  return ftz(prod + acc);
+#elif ORC_SABOTAGE == 5
+  const double exact = (double)fa * (double)fb + (double)acc;
+  if (exact != 0.0 && fabs(exact) < 0x1p-126) return exact < 0.0 ? -0.0f : 0.0f;
+  return ftz(fmaf(fa, fb, acc));
+#elif ORC_SABOTAGE == 12
+  return fmaf(fa, fb, acc);
+#else
+  return ftz(fmaf(fa, fb, acc));
+#endif
+}
+
 static float leaf_partial(const float* a, const float* b, int op, int64_t i, int64_t j, int64_t m,
                           int64_t n, int64_t k, int64_t p0, int64_t p1) {
+#if ORC_SABOTAGE == 8
+  float acc = -0.0f;
+#else
   float acc = 0.0f;
-  for (int64_t p = p0; p < p1; ++p)
-    acc = ftz(fmaf(ftz(a_at(a, op, i, p, m, k)), ftz(b_at(b, op, p, j, n, k)), acc));
+#endif
+  for (int64_t p = p0; p < p1; ++p) acc = chain_step(a_at(a, op, i, p, m, k), b_at(b, op, p, j, n, k), acc);
   return ftz(acc);
 }
 
@@ -98,14 +156,29 @@ static float leaf_partial(const float* a, const float* b, int op, int64_t i, int
  * overwritten (it is the level being reduced in place: next[q] lands in cur[q]). */
 float orc_fold_tree(float* buf, int64_t p) {
   if (p <= 0) return 0.0f;
+#if ORC_SABOTAGE == 3
+  float s = buf[0];
+  for (int64_t t = 1; t < p; ++t) s = ftz(ftz(s) + ftz(buf[t]));
+  return ftz(s);
+#else
   int64_t width = p;
   while (width > 1) {
     int64_t pairs = width / 2;
+#if ORC_SABOTAGE == 1
+    for (int64_t q = 0; q < pairs; ++q) buf[q] = ftz(ftz(buf[q]) + ftz(buf[q + (width + 1) / 2]));
+    if (width & 1) buf[pairs] = buf[pairs];
+#else
     for (int64_t q = 0; q < pairs; ++q) buf[q] = ftz(ftz(buf[2 * q]) + ftz(buf[2 * q + 1]));
+#if ORC_SABOTAGE == 2
+    if (width & 1) buf[pairs] = ftz(ftz(buf[width - 1]) + 0.0f);
+#else
     if (width & 1) buf[pairs] = buf[width - 1]; /* the carry: bit for bit */
+#endif
+#endif
     width = pairs + (width & 1);
   }
   return ftz(buf[0]);
+#endif
 }
 
 /* The register-stack realisation of the same tree (what the device kernels and the
@@ -245,6 +318,11 @@ static float fast_cell(const float* ae, const float* be, int64_t ldb, int64_t j,
  * are spread over threads.  Output bits equal orc_gemm's. */
 void orc_gemm_fast(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k,
                    int op, int64_t leaf, int nthreads) {
+#if ORC_SABOTAGE != 0
+  (void)nthreads;
+  orc_gemm(c, a, b, m, n, k, op, leaf);
+  return;
+#endif
   if (leaf <= 0) leaf = orc_leaf_size(k);
   int64_t pc = orc_leaf_count(k, leaf);
   if (nthreads <= 0) nthreads = omp_get_max_threads();
@@ -277,17 +355,237 @@ void orc_gemm_fast(float* c, const float* a, const float* b, int64_t m, int64_t 
   free(be);
 }
 
+/* ---------------- the reference's fast CPU column: gemm_host_rows ----------------
+ * gemm/host/gemm_host_rows.mojo restated.  The arithmetic is orc_gemm's, cell for cell; what
+ * changes is around it:
+ *  - operands flushed once into packed copies: A_eff row-major [m][k]; B_eff as panels of
+ *    GHR_G = 32 columns, each [k][32] contiguous, columns past n +0.0 (:232-288);
+ *  - one panel's 32 cells of a row advance together as GHR_CHAINS = 4 AVX2 vectors of 8, one
+ *    lane per cell, each lane one IEEE fma per step (:163-190);
+ *  - the per-step flush DEFERRED: every raw result goes into the tracker
+ *    min((bits - 1) & 0x7FFFFFFF), below 0x007FFFFF exactly when some raw result was
+ *    subnormal (both zeros wrap high); then the panel is recomputed with a flush at every step
+ *    (:120-131,185-198).  Operands are flushed, so only an accumulator can be subnormal, and
+ *    where none was, ftz was the identity at every step;
+ *  - the leaf partials folded in place level by level, an odd level's last row carried
+ *    (:203-225);
+ *  - m <= 4: no packing, B read in place, a flush at every step (:364-437);
+ *  - tasks split the packing, then the cells by rows (m >= 2 tasks) or by panels (:509-551).
+ * A NaN's payload may differ from orc_gemm's (x86 fma propagates the NaN of whichever operand
+ * the compiler put first); after NaN canonicalization the words are orc_gemm's. */
+#define GHR_FW 8
+#define GHR_CHAINS 4
+#define GHR_G (GHR_FW * GHR_CHAINS)
+#define GHR_SMALL_M 4
+
+static void ghr_pack_a(const float* a, int op, int64_t m, int64_t k, float* ap, int64_t lo, int64_t hi) {
+  for (int64_t i = lo; i < hi; ++i)
+    for (int64_t p = 0; p < k; ++p) ap[i * k + p] = ftz(a_at(a, op, i, p, m, k));
+}
+
+static void ghr_pack_b(const float* b, int op, int64_t n, int64_t k, float* bp, int64_t glo, int64_t ghi) {
+  for (int64_t g = glo; g < ghi; ++g) {
+    const int64_t j0 = g * GHR_G;
+    const int64_t width = n - j0 < GHR_G ? n - j0 : GHR_G;
+    float* panel = bp + g * k * GHR_G;
+    for (int64_t p = 0; p < k; ++p)
+      for (int64_t jj = 0; jj < GHR_G; ++jj)
+        panel[p * GHR_G + jj] = jj < width ? ftz(b_at(b, op, p, j0 + jj, n, k)) : 0.0f;
+  }
+}
+
+/* One panel's 32 cells over the leaf [pb, pe): dst[jj] = the leaf partial of column j0 + jj. */
+static void ghr_panel_chain(const float* arow, const float* panel, int64_t pb, int64_t pe, float* dst,
+                           int force_redo) {
+  const __m256i one = _mm256_set1_epi32(1);
+  const __m256i absm = _mm256_set1_epi32(0x7FFFFFFF);
+  __m256 c[GHR_CHAINS];
+  __m256i e[GHR_CHAINS];
+  for (int q = 0; q < GHR_CHAINS; ++q) {
+    c[q] = _mm256_setzero_ps();
+    e[q] = _mm256_set1_epi32(-1);
+  }
+  for (int64_t p = pb; p < pe; ++p) {
+    const __m256 sv = _mm256_set1_ps(arow[p]);
+    for (int q = 0; q < GHR_CHAINS; ++q) {
+      const __m256 raw = _mm256_fmadd_ps(sv, _mm256_loadu_ps(panel + p * GHR_G + q * GHR_FW), c[q]);
+      e[q] = _mm256_min_epu32(e[q], _mm256_and_si256(_mm256_sub_epi32(_mm256_castps_si256(raw), one), absm));
+      c[q] = raw;
+    }
+  }
+  __m256i emin = _mm256_min_epu32(_mm256_min_epu32(e[0], e[1]), _mm256_min_epu32(e[2], e[3]));
+  /* tracked values are below 2^31, so a signed compare orders them */
+  const int sub = _mm256_movemask_epi8(_mm256_cmpgt_epi32(_mm256_set1_epi32(0x007FFFFF), emin)) != 0;
+  int redo = force_redo || sub;
+#if ORC_SABOTAGE == 13
+  redo = 0;
+#endif
+  if (redo) {
+    for (int q = 0; q < GHR_CHAINS; ++q) {
+      __m256 acc = _mm256_setzero_ps();
+      for (int64_t p = pb; p < pe; ++p)
+        acc = vftz(_mm256_fmadd_ps(_mm256_set1_ps(arow[p]), _mm256_loadu_ps(panel + p * GHR_G + q * GHR_FW), acc));
+      _mm256_storeu_ps(dst + q * GHR_FW, acc);
+    }
+    return;
+  }
+  for (int q = 0; q < GHR_CHAINS; ++q) _mm256_storeu_ps(dst + q * GHR_FW, c[q]);
+}
+
+/* The balanced tree over `pcount` rows of `width` partials at sp, in place, root in row 0. */
+static void ghr_fold_in_place(float* sp, int64_t pcount, int64_t width) {
+  int64_t w = pcount;
+  while (w > 1) {
+    const int64_t pairs = w / 2;
+    for (int64_t q = 0; q < pairs; ++q) {
+      float* dst = sp + q * width;
+      const float* l = sp + 2 * q * width;
+      const float* r = l + width;
+      int64_t j = 0;
+      for (; j + GHR_FW <= width; j += GHR_FW)
+        _mm256_storeu_ps(dst + j, vftz(_mm256_add_ps(_mm256_loadu_ps(l + j), _mm256_loadu_ps(r + j))));
+      for (; j < width; ++j) dst[j] = ftz(l[j] + r[j]);
+    }
+    if (w & 1) memmove(sp + pairs * width, sp + (w - 1) * width, sizeof(float) * (size_t)width); /* the carry */
+    w = pairs + (w & 1);
+  }
+}
+
+static void ghr_tile(const float* ap, const float* bp, float* c, int64_t n, int64_t k, int64_t lo, int64_t hi,
+                     int64_t glo, int64_t ghi, int force_redo) {
+  const int64_t leaf = orc_leaf_size(k), pcount = orc_leaf_count(k, leaf);
+  float* scratch = (float*)malloc(sizeof(float) * (size_t)(pcount * GHR_G));
+  for (int64_t g = glo; g < ghi; ++g) {
+    const float* panel = bp + g * k * GHR_G;
+    const int64_t j0 = g * GHR_G;
+    const int64_t width = n - j0 < GHR_G ? n - j0 : GHR_G;
+    for (int64_t i = lo; i < hi; ++i) {
+      for (int64_t t = 0; t < pcount; ++t) {
+        const int64_t pb = t * leaf, pe = pb + leaf < k ? pb + leaf : k;
+        ghr_panel_chain(ap + i * k, panel, pb, pe, scratch + t * GHR_G, force_redo);
+      }
+      if (pcount > 1) ghr_fold_in_place(scratch, pcount, GHR_G);
+      memcpy(c + i * n + j0, scratch, sizeof(float) * (size_t)width);
+    }
+  }
+  free(scratch);
+}
+
+/* m <= 4: columns [jlo, jhi), B read in place, a flush at every step. */
+static void ghr_small_m(const float* a, const float* b, float* c, int op, int64_t m, int64_t n, int64_t k,
+                        int64_t jlo, int64_t jhi) {
+  const int64_t leaf = orc_leaf_size(k), pcount = orc_leaf_count(k, leaf);
+  const int64_t width = m * GHR_FW;
+  float* scratch = (float*)malloc(sizeof(float) * (size_t)(pcount * width));
+  for (int64_t j0 = jlo; j0 < jhi; j0 += GHR_FW) {
+    const int full = j0 + GHR_FW <= jhi;
+    for (int64_t t = 0; t < pcount; ++t) {
+      const int64_t pb = t * leaf, pe = pb + leaf < k ? pb + leaf : k;
+      float* dst = scratch + t * width;
+      if (full) {
+        __m256 acc[GHR_SMALL_M];
+        for (int64_t i = 0; i < m; ++i) acc[i] = _mm256_setzero_ps();
+        for (int64_t p = pb; p < pe; ++p) {
+          float bv[GHR_FW];
+          for (int r = 0; r < GHR_FW; ++r) bv[r] = ftz(b_at(b, op, p, j0 + r, n, k));
+          const __m256 bw = _mm256_loadu_ps(bv);
+          for (int64_t i = 0; i < m; ++i)
+            acc[i] = vftz(_mm256_fmadd_ps(_mm256_set1_ps(ftz(a_at(a, op, i, p, m, k))), bw, acc[i]));
+        }
+        for (int64_t i = 0; i < m; ++i) _mm256_storeu_ps(dst + i * GHR_FW, acc[i]);
+      } else {
+        for (int64_t i = 0; i < m; ++i)
+          for (int64_t jj = 0; jj < GHR_FW; ++jj) {
+            float acc = 0.0f;
+            if (j0 + jj < jhi)
+              for (int64_t p = pb; p < pe; ++p)
+                acc = ftz(fmaf(ftz(a_at(a, op, i, p, m, k)), ftz(b_at(b, op, p, j0 + jj, n, k)), acc));
+            dst[i * GHR_FW + jj] = acc;
+          }
+      }
+    }
+    if (pcount > 1) ghr_fold_in_place(scratch, pcount, width);
+    const int64_t cnt = jhi - j0 < GHR_FW ? jhi - j0 : GHR_FW;
+    for (int64_t i = 0; i < m; ++i) memcpy(c + i * n + j0, scratch + i * GHR_FW, sizeof(float) * (size_t)cnt);
+  }
+  free(scratch);
+}
+
+/* gemm/host/gemm_host_rows.mojo:492-556 gemm_host_rows_into: C = op(A) . op(B), the bits of
+ * orc_gemm, on `nthreads` threads (0 = all).  `force_redo` takes the flushed recomputation on
+ * every panel (the reference's check of its redo path). */
+void orc_host_rows(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int op,
+                   int nthreads, int force_redo) {
+#if ORC_SABOTAGE != 0 && ORC_SABOTAGE != 13
+  (void)nthreads;
+  (void)force_redo;
+  orc_gemm(c, a, b, m, n, k, op, 0);
+  return;
+#endif
+  if (m <= 0 || n <= 0) return;
+  if (nthreads <= 0) nthreads = omp_get_max_threads();
+  if (k <= 0) {
+    for (int64_t i = 0; i < m * n; ++i) c[i] = 0.0f;
+    return;
+  }
+  if (m <= GHR_SMALL_M) {
+    const int64_t blocks = (n + GHR_FW - 1) / GHR_FW;
+    const int64_t chunk = (blocks + nthreads - 1) / nthreads;
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int t = 0; t < nthreads; ++t) {
+      const int64_t lo = t * chunk * GHR_FW, hi = (t + 1) * chunk * GHR_FW;
+      if (lo < n) ghr_small_m(a, b, c, op, m, n, k, lo, hi < n ? hi : n);
+    }
+    return;
+  }
+  const int64_t npan = (n + GHR_G - 1) / GHR_G;
+  float* ap = (float*)malloc(sizeof(float) * (size_t)(m * k));
+  float* bp = (float*)malloc(sizeof(float) * (size_t)(npan * k * GHR_G));
+  const int64_t rchunk = (m + nthreads - 1) / nthreads, pchunk = (npan + nthreads - 1) / nthreads;
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+  for (int t = 0; t < nthreads; ++t) {
+    const int64_t r0 = t * rchunk, r1 = (t + 1) * rchunk < m ? (t + 1) * rchunk : m;
+    const int64_t g0 = t * pchunk, g1 = (t + 1) * pchunk < npan ? (t + 1) * pchunk : npan;
+    if (r0 < r1) ghr_pack_a(a, op, m, k, ap, r0, r1);
+    if (g0 < g1) ghr_pack_b(b, op, n, k, bp, g0, g1);
+  }
+  const int by_rows = m >= 2 * (int64_t)nthreads;
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+  for (int t = 0; t < nthreads; ++t) {
+    if (by_rows) {
+      const int64_t r0 = t * rchunk, r1 = (t + 1) * rchunk < m ? (t + 1) * rchunk : m;
+      if (r0 < r1) ghr_tile(ap, bp, c, n, k, r0, r1, 0, npan, force_redo);
+    } else {
+      const int64_t g0 = t * pchunk, g1 = (t + 1) * pchunk < npan ? (t + 1) * pchunk : npan;
+      if (g0 < g1) ghr_tile(ap, bp, c, n, k, 0, m, g0, g1, force_redo);
+    }
+  }
+  free(ap);
+  free(bp);
+}
+
 /* ---------------- seams around the product ---------------- */
 
 /* transformer/impl/llama/modeling_llama.mojo:3979-3989: y = ftz(ftz(y) + ftz(b[col])). */
 void orc_bias(float* y, const float* bias, int64_t m, int64_t n) {
   for (int64_t i = 0; i < m; ++i)
-    for (int64_t j = 0; j < n; ++j) y[i * n + j] = ftz(ftz(y[i * n + j]) + ftz(bias[j]));
+    for (int64_t j = 0; j < n; ++j) {
+#if ORC_SABOTAGE == 10
+      y[i * n + j] = ftz(y[i * n + j] + bias[j]);
+#else
+      y[i * n + j] = ftz(ftz(y[i * n + j]) + ftz(bias[j]));
+#endif
+    }
 }
 
 /* core/nan_canon.mojo:55-110: every NaN word becomes 0x7FC00000, nothing else moves. */
 void orc_nan_canon(float* x, int64_t count) {
   uint32_t* w = (uint32_t*)x;
+#if ORC_SABOTAGE == 9
+  (void)w;
+  (void)count;
+  return;
+#endif
   for (int64_t i = 0; i < count; ++i)
     if ((w[i] & 0x7FFFFFFFu) > 0x7F800000u) w[i] = 0x7FC00000u;
 }
@@ -320,7 +618,11 @@ void orc_int8_dequant(float* out, const int8_t* codes, const float* scales, int6
   for (int64_t p = 0; p < k; ++p)
     for (int64_t j = 0; j < n; ++j) {
       int64_t idx = op == OP_NT ? j * k + p : p * n + j;
+#if ORC_SABOTAGE == 11
+      out[idx] = ftz((float)codes[idx] * scales[j]);
+#else
       out[idx] = ftz((float)codes[idx] * ftz(scales[j]));
+#endif
     }
 }
 

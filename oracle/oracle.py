@@ -19,9 +19,46 @@ _lib = None
 OP_NN, OP_NT, OP_TN = 0, 1, 2
 
 
-def build():
-    """Compile liboracle.so in place (gcc; see oracle/Makefile)."""
+def build(sabotage=False):
+    """Compile liboracle.so in place (gcc; see oracle/Makefile); with `sabotage`, also the
+    planted-mistake variants under oracle/_sabotage/."""
     subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+    if sabotage:
+        build_sabotage()
+
+
+#: The planted mistakes of gemm_oracle.c (ORC_SABOTAGE = n), by name.
+SABOTAGE = {1: "fold_stride_pairs", 2: "fold_pad_zero", 3: "fold_serial", 4: "step_unfused",
+            5: "step_flush_before_round", 6: "operands_unflushed", 7: "leaf_from_tile",
+            8: "seed_minus_zero", 9: "no_nan_canon", 10: "bias_unflushed", 11: "scale_unflushed",
+            12: "accumulator_unflushed", 13: "host_rows_no_redo"}
+
+
+def sabotage_path(n):
+    return os.path.join(_HERE, "_sabotage", f"liboracle_s{n}.so")
+
+
+def build_sabotage():
+    subprocess.run(["make", "-s", "-C", _HERE, "sabotage"], check=True)
+
+
+class using:
+    """Within the block, every function of this module calls the library at `path` (a
+    planted-mistake variant) instead of liboracle.so."""
+
+    def __init__(self, path):
+        self.path = path
+
+    def __enter__(self):
+        global _lib
+        self._saved = _lib
+        _lib = _configure(ctypes.CDLL(self.path))
+        return self
+
+    def __exit__(self, *exc):
+        global _lib
+        _lib = self._saved
+        return False
 
 
 def lib():
@@ -29,47 +66,51 @@ def lib():
     if _lib is None:
         if not os.path.exists(_LIB_PATH):
             build()
-        L = ctypes.CDLL(_LIB_PATH)
-        i64, vp, c_int, f32 = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_float
-        L.orc_leaf_size.argtypes = [i64]; L.orc_leaf_size.restype = i64
-        L.orc_leaf_count.argtypes = [i64, i64]; L.orc_leaf_count.restype = i64
-        L.orc_gemm.argtypes = [vp, vp, vp, i64, i64, i64, c_int, i64]; L.orc_gemm.restype = None
-        L.orc_gemm_serial.argtypes = [vp, vp, vp, i64, i64, i64, c_int]; L.orc_gemm_serial.restype = None
-        L.orc_gemm_fast.argtypes = [vp, vp, vp, i64, i64, i64, c_int, i64, c_int]; L.orc_gemm_fast.restype = None
-        L.orc_fold_tree.argtypes = [vp, i64]; L.orc_fold_tree.restype = f32
-        L.orc_fold_stack.argtypes = [vp, i64]; L.orc_fold_stack.restype = f32
-        L.orc_bias.argtypes = [vp, vp, i64, i64]; L.orc_bias.restype = None
-        L.orc_nan_canon.argtypes = [vp, i64]; L.orc_nan_canon.restype = None
-        L.orc_bf16_widen.argtypes = [vp, vp, i64]; L.orc_bf16_widen.restype = None
-        L.orc_bf16_narrow.argtypes = [vp, vp, i64]; L.orc_bf16_narrow.restype = None
-        L.orc_int8_dequant.argtypes = [vp, vp, vp, i64, i64, c_int]; L.orc_int8_dequant.restype = None
-        L.orc_fnv1a64.argtypes = [vp, i64]; L.orc_fnv1a64.restype = ctypes.c_uint64
-        L.orc_q8_i32_to_f32.argtypes = [ctypes.c_int32]; L.orc_q8_i32_to_f32.restype = f32
-        L.orc_q8_row_exponent.argtypes = [f32]; L.orc_q8_row_exponent.restype = c_int
-        L.orc_q8_quantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_quantize_rows.restype = None
-        L.orc_q8_dequantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_dequantize_rows.restype = None
-        L.orc_q8_gemm.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q8_gemm.restype = None
-        L.orc_q15_i64_to_f32.argtypes = [i64]; L.orc_q15_i64_to_f32.restype = f32
-        L.orc_q15_row_exponent.argtypes = [f32]; L.orc_q15_row_exponent.restype = c_int
-        L.orc_q15_quantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_quantize_rows.restype = None
-        L.orc_q15_dequantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_dequantize_rows.restype = None
-        L.orc_q15_gemm.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q15_gemm.restype = None
-        L.orc_f16_widen.argtypes = [vp, vp, i64]; L.orc_f16_widen.restype = None
-        L.orc_card_fill.argtypes = [vp, i64, i64]; L.orc_card_fill.restype = None
-        L.orc_ftz.argtypes = [f32]; L.orc_ftz.restype = f32
-        L.orc_fma.argtypes = [f32, f32, f32]; L.orc_fma.restype = f32
-        L.orc_max_threads.argtypes = []; L.orc_max_threads.restype = c_int
-        L.orc_seq_gemm.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, c_int]
-        L.orc_seq_gemm.restype = None
-        L.orc_epilogue.argtypes = [vp, i64, i64, i64, c_int, vp, c_int]; L.orc_epilogue.restype = None
-        L.orc_map.argtypes = [vp, vp, i64, c_int]; L.orc_map.restype = None
-        for name in ("orc_expf", "orc_sigmoidf", "orc_tanhf"):
-            getattr(L, name).argtypes = [f32]
-            getattr(L, name).restype = f32
-        L.orc_act_value.argtypes = [f32, c_int]; L.orc_act_value.restype = f32
-        L.orc_act_bwd_value.argtypes = [f32, f32, c_int]; L.orc_act_bwd_value.restype = f32
-        _lib = L
+        _lib = _configure(ctypes.CDLL(_LIB_PATH))
     return _lib
+
+
+def _configure(L):
+    i64, vp, c_int, f32 = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    L.orc_leaf_size.argtypes = [i64]; L.orc_leaf_size.restype = i64
+    L.orc_leaf_count.argtypes = [i64, i64]; L.orc_leaf_count.restype = i64
+    L.orc_gemm.argtypes = [vp, vp, vp, i64, i64, i64, c_int, i64]; L.orc_gemm.restype = None
+    L.orc_gemm_serial.argtypes = [vp, vp, vp, i64, i64, i64, c_int]; L.orc_gemm_serial.restype = None
+    L.orc_gemm_fast.argtypes = [vp, vp, vp, i64, i64, i64, c_int, i64, c_int]; L.orc_gemm_fast.restype = None
+    L.orc_fold_tree.argtypes = [vp, i64]; L.orc_fold_tree.restype = f32
+    L.orc_fold_stack.argtypes = [vp, i64]; L.orc_fold_stack.restype = f32
+    L.orc_bias.argtypes = [vp, vp, i64, i64]; L.orc_bias.restype = None
+    L.orc_nan_canon.argtypes = [vp, i64]; L.orc_nan_canon.restype = None
+    L.orc_bf16_widen.argtypes = [vp, vp, i64]; L.orc_bf16_widen.restype = None
+    L.orc_bf16_narrow.argtypes = [vp, vp, i64]; L.orc_bf16_narrow.restype = None
+    L.orc_int8_dequant.argtypes = [vp, vp, vp, i64, i64, c_int]; L.orc_int8_dequant.restype = None
+    L.orc_fnv1a64.argtypes = [vp, i64]; L.orc_fnv1a64.restype = ctypes.c_uint64
+    L.orc_q8_i32_to_f32.argtypes = [ctypes.c_int32]; L.orc_q8_i32_to_f32.restype = f32
+    L.orc_q8_row_exponent.argtypes = [f32]; L.orc_q8_row_exponent.restype = c_int
+    L.orc_q8_quantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_quantize_rows.restype = None
+    L.orc_q8_dequantize_rows.argtypes = [vp, vp, vp, i64, i64]; L.orc_q8_dequantize_rows.restype = None
+    L.orc_q8_gemm.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q8_gemm.restype = None
+    L.orc_q15_i64_to_f32.argtypes = [i64]; L.orc_q15_i64_to_f32.restype = f32
+    L.orc_q15_row_exponent.argtypes = [f32]; L.orc_q15_row_exponent.restype = c_int
+    L.orc_q15_quantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_quantize_rows.restype = None
+    L.orc_q15_dequantize_rows.argtypes = [vp, vp, vp, vp, i64, i64]; L.orc_q15_dequantize_rows.restype = None
+    L.orc_q15_gemm.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64]; L.orc_q15_gemm.restype = None
+    L.orc_f16_widen.argtypes = [vp, vp, i64]; L.orc_f16_widen.restype = None
+    L.orc_card_fill.argtypes = [vp, i64, i64]; L.orc_card_fill.restype = None
+    L.orc_ftz.argtypes = [f32]; L.orc_ftz.restype = f32
+    L.orc_fma.argtypes = [f32, f32, f32]; L.orc_fma.restype = f32
+    L.orc_max_threads.argtypes = []; L.orc_max_threads.restype = c_int
+    L.orc_seq_gemm.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, c_int]
+    L.orc_seq_gemm.restype = None
+    L.orc_epilogue.argtypes = [vp, i64, i64, i64, c_int, vp, c_int]; L.orc_epilogue.restype = None
+    L.orc_map.argtypes = [vp, vp, i64, c_int]; L.orc_map.restype = None
+    for name in ("orc_expf", "orc_sigmoidf", "orc_tanhf"):
+        getattr(L, name).argtypes = [f32]
+        getattr(L, name).restype = f32
+    L.orc_act_value.argtypes = [f32, c_int]; L.orc_act_value.restype = f32
+    L.orc_act_bwd_value.argtypes = [f32, f32, c_int]; L.orc_act_bwd_value.restype = f32
+    L.orc_host_rows.argtypes = [vp, vp, vp, i64, i64, i64, c_int, c_int, c_int]; L.orc_host_rows.restype = None
+    return L
 
 
 def _p(x):
@@ -127,6 +168,16 @@ def gemm_fast(a, b, op=OP_NN, leaf=0, threads=0):
     m, n, k = _shape(a, b, op)
     c = np.empty((m, n), np.float32)
     lib().orc_gemm_fast(_p(c), _p(a), _p(b), m, n, k, op, leaf, threads)
+    return c
+
+
+def host_rows(a, b, op=OP_NN, threads=0, force_redo=False):
+    """gemm/host/gemm_host_rows.mojo:492-556 `gemm_host_rows_into`: orc_gemm's bits (NaN words
+    equal after canonicalization) with the deferred flush and its redo, on `threads` threads."""
+    a, b = _f32c(a), _f32c(b)
+    m, n, k = _shape(a, b, op)
+    c = np.empty((m, n), np.float32)
+    lib().orc_host_rows(_p(c), _p(a), _p(b), m, n, k, op, threads, 1 if force_redo else 0)
     return c
 
 

@@ -197,3 +197,36 @@ def test_lowbit_repack_same_format_copies_without_materializing(monkeypatch, fmt
         assert np.array_equal(copied.codes, original.codes) and not np.shares_memory(copied.codes, original.codes)
         assert np.array_equal(copied.exponents, original.exponents)
         assert not np.shares_memory(copied.exponents, original.exponents)
+
+
+def test_route_names_the_kernels_without_a_device():
+    """mlg_gemm_route (num_cus > 0: no device needed) for the five workloads and the skinny
+    matrix-core shapes: the dispatcher's choices as the design states them."""
+    from mojolearn_amd import device as D
+    R = lambda *a, **k: D.route(*a, num_cus=256, **k)  # noqa: E731
+    assert R(2048, 4096, 4096) == {"tile", "tile_stack"}  # 512 tiles, 32 leaves folded in each tile
+    assert R(512, 512, 512) == {"tile", "fold"}  # 16 tiles: 4 leaf groups, then the fold
+    assert R(512, 50304, 2048) == {"tile", "tile_stack", "fold", "tail_split"}
+    assert R(4096, 11008, 4096, b_type=D.T_BF16) == {"tile", "tile_stack"}
+    assert R(1, 14336, 4096, b_type=D.T_I8) == {"gemv_nn", "gemv_groups"}
+    assert R(4, 14336, 4096, b_type=D.T_I8) == {"mfma4", "gemv_groups"}
+    assert R(16, 14336, 4096, b_type=D.T_I8) == {"mfma16", "gemv_groups"}
+    assert R(1, 14336, 4096, op=D.OP_NT) == {"gemv_nt", "gemv_groups"}
+    assert R(1, 64, 128) == {"gemv_nn"}  # one leaf group: no cross-workgroup fold
+    assert R(3, 5, 0) == {"zero_k"}
+    assert R(16, 64, 4096, a=4) == {"gemv_nn", "gemv_groups"}  # x off the 16-byte grid: the VALU kernel
+    assert "repack" in R(64, 64, 100, a=4)
+
+
+def test_launch_limits_are_refused_with_a_message():
+    """Partitions past the fold stack (2^20 roots per cell) or past a tile grid's leaf-group
+    column (65535) are refused, never computed wrong (the reference refuses partitions past its
+    fold stack, gemm/neural_dispatch.mojo:284-285)."""
+    from mojolearn_amd import device as D
+    assert D.route(1, 64, 4 * (1 << 20), leaf=1, num_cus=256) == {"gemv_nn", "gemv_groups"}
+    with pytest.raises(RuntimeError, match="fold stack"):
+        D.route(1, 64, 4 * (1 << 20) + 1, leaf=1, num_cus=256)
+    # a tile groups up to 32 leaves: 65535 groups hold 2,097,120 leaves
+    assert "fold" in D.route(17, 17, 65535 * 32, leaf=1, num_cus=256)
+    with pytest.raises(RuntimeError, match="grid column"):
+        D.route(17, 17, 65535 * 32 + 1, leaf=1, num_cus=256)

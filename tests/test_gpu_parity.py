@@ -25,12 +25,18 @@ def _dev():
     return device
 
 
+POISON = -987654.0  # gemm/checks/gemm_device_check.mojo:111: a cell left unwritten fails
+
+
 def gpu_gemm(a, b, op, leaf=0, bias=None):
     D = _dev()
     ta = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     tb = torch.from_numpy(np.ascontiguousarray(b)).to(DEV)
     tbias = None if bias is None else torch.from_numpy(np.ascontiguousarray(bias)).to(DEV)
-    c = D.gemm(ta, tb, op=op, leaf=leaf, bias=tbias)
+    m = a.shape[1] if op == 2 else a.shape[0]
+    n = b.shape[0] if op == 1 else b.shape[1]
+    out = torch.full((m, n), POISON, dtype=torch.float32, device=DEV)
+    c = D.gemm(ta, tb, op=op, leaf=leaf, bias=tbias, out=out)
     torch.cuda.synchronize()
     return c.cpu().numpy()
 
