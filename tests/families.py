@@ -206,14 +206,15 @@ def kat_cases(cus=256):
             padded = kp != k
             for c0 in range(0, len(fxs), m):
                 chunk = fxs[c0:c0 + m]
-                plants = [(t, (5 * t + 2) % n, want) for t, (_, _, _, want) in enumerate(chunk)] if not padded else []
+                assert 2 + 4 * (len(chunk) - 1) < n  # one column per fixture
+                plants = [(t, 2 + 4 * t, want) for t, (_, _, _, want) in enumerate(chunk)] if not padded else []
 
                 def make(chunk=chunk, seed=k * 131 + c0 + op + m, m=m, n=n, k=k, kp=kp, op=op):
                     rng = np.random.default_rng(seed)
                     A = _filler(rng, (m, kp))
                     B = _filler(rng, (kp, n))
                     for t, (_, fa, fb, _) in enumerate(chunk):
-                        col = (5 * t + 2) % n
+                        col = 2 + 4 * t
                         A[t] = 0.0
                         B[:, col] = 0.0
                         A[t, :k] = fa

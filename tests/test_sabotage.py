@@ -92,3 +92,18 @@ def test_honest_oracle_passes_the_same_pins(oracle):
     PINS.test_bias_against_numpy_words(oracle)
     PINS.test_int8_dequant_against_numpy(oracle, 0)
     PINS.test_host_rows_equals_oracle(oracle, (40, 100, 1000), 0)
+
+
+def test_family_plants_hold_on_the_oracle(oracle):
+    """Every planted fixture cell of the family cases holds its closed-form word on the oracle
+    (the tile_stack copies of these products differ only in their column count)."""
+    checked = 0
+    for case in F.kat_cases():
+        if case.family == "tile_stack":
+            continue
+        w = _words(case.want(oracle))
+        for r, c, word in case.plants:
+            assert w[r, c] == word, (case.id, r, c, hex(int(w[r, c])), hex(int(word)))
+            checked += 1
+        case.release()
+    assert checked > 300
