@@ -107,6 +107,18 @@ int mlg_gemm_ws(float* c, const void* a, const void* b, const float* scales, con
                 int64_t m, int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type,
                 int64_t leaf, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* mlg_gemm_ws with no workspace argument, for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The workspace is the library's own scratch array, 32 MiB per GPU (a static device
+ * array, held from the library's load on that GPU until the process ends); a product that needs
+ * more (mlg_gemm_workspace_bytes_for) is refused with an error.  The call allocates and frees
+ * nothing and never synchronizes; it clears the array's completion counters with a kernel on
+ * `stream` first.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two threads, two graphs replayed at once) race and must be ordered by the
+ * caller. */
+int mlg_gemm_noalloc(float* c, const void* a, const void* b, const float* scales, const float* bias, int64_t m,
+                     int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type, int64_t leaf, void* stream);
+
 /* Bytes of workspace mlg_gemm_ws needs for this product on the current device, for operands
  * a, b at these addresses (an operand the tile kernel cannot load in place -- base not 16-byte
  * aligned, rows not a multiple of 16 bytes -- is repacked into the workspace); -1 on error.

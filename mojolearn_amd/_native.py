@@ -53,6 +53,8 @@ def lib():
         L.mlg_gemm_int8w.restype = ctypes.c_int
         L.mlg_gemm_ws.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i32, i64, vp, i64, vp]
         L.mlg_gemm_ws.restype = ctypes.c_int
+        L.mlg_gemm_noalloc.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i32, i64, vp]
+        L.mlg_gemm_noalloc.restype = ctypes.c_int
         L.mlg_gemm_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i32, i64]
         L.mlg_gemm_workspace_bytes.restype = i64
         L.mlg_gemm_workspace_bytes_for.argtypes = [vp, vp, i64, i64, i64, i32, i32, i32, i64]

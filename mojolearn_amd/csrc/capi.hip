@@ -736,6 +736,64 @@ int mlg_gemm_ws(float* c, const void* a, const void* b, const float* scales, con
   });
 }
 
+}  // extern "C"
+
+namespace {
+
+// The workspace of mlg_gemm_noalloc: one array per GPU, held from the code object's load until
+// the process ends.  In host code `scratch` names a host-side stand-in, never device memory: the
+// entry uses only the address hipGetSymbolAddress gives for the current device.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t(32) << 20;
+static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
+
+// This device's address of `scratch`, looked up once per device with that device current.
+void* scratch_on_current_device() {
+  constexpr int MAX_DEVICES = 64;
+  static std::mutex mu;
+  static void* ptr[MAX_DEVICES] = {};
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= MAX_DEVICES) throw Fail("mlg_gemm_noalloc: device ordinal out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) throw Fail("mlg_gemm_noalloc: hipGetSymbolAddress gave no address for the scratch array");
+    ptr[dev] = p;
+  }
+  return ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlg_gemm_noalloc(float* c, const void* a, const void* b, const float* scales, const float* bias, int64_t m,
+                     int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type, int64_t leaf, void* stream) {
+  return guarded([&] {
+    if (a_type != mlg::T_F32 && a_type != mlg::T_BF16) throw Fail("mlgemm: a_type must be 0 (f32) or 1 (bf16)");
+    if (b_type < mlg::T_F32 || b_type > mlg::T_I8) throw Fail("mlgemm: b_type must be 0 (f32), 1 (bf16) or 2 (int8)");
+    if (a_type == mlg::T_BF16 && b_type != mlg::T_BF16) throw Fail("mlgemm: a bf16 A needs a bf16 B");
+    mlg::GemmProblem p{};
+    p.c = c; p.a = a; p.b = b; p.scales = scales; p.bias = bias; p.m = m; p.n = n; p.k = k; p.op = op;
+    p.a_type = a_type; p.b_type = b_type; p.leaf = leaf;
+    const int cus = num_cus_of_current_device();
+    check_problem(p, cus);
+    if (p.m == 0 || p.n == 0) return;
+    const int64_t need = mlg::gemm_workspace_floats(p, cus) * (int64_t)sizeof(float);
+    if (need > NOALLOC_SCRATCH_BYTES)
+      throw Fail("mlg_gemm_noalloc: this product needs " + std::to_string(need) + " bytes of workspace, more than the " +
+                 std::to_string(NOALLOC_SCRATCH_BYTES) + " of the library's scratch array; use mlg_gemm_ws");
+    void* ws = need > 0 ? scratch_on_current_device() : nullptr;
+    // the array keeps the last call's contents: its completion counters start at zero here
+    // (a kernel, not a memset: the call may be captured in a graph)
+    const int64_t ncnt = mlg::gemm_counter_count(p);
+    if (ncnt > 0) hip_check(mlg::run_zero_words(static_cast<unsigned int*>(ws), ncnt, (hipStream_t)stream),
+                            "counter clear launch");
+    enqueue_gemm(p, (hipStream_t)stream, ws, need);
+  });
+}
+
 int mlg_bf16_widen(float* out, const uint16_t* in, int64_t count, void* stream) {
   return guarded([&] { hip_check(mlg::run_bf16_widen(out, in, count, (hipStream_t)stream), "from_bf16 launch"); });
 }
