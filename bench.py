@@ -237,16 +237,18 @@ def cpu_baseline(W, O, gpu_out=None, min_seconds=10.0, max_seconds=30.0):
 
 
 class _SeqLinear:
-    """The sequence executor's linear step (sequence/ops.mojo:485-569): op_gemm, one whole-k chain
-    per cell into `out`, then the bias + activation follower over it."""
+    """The sequence executor's linear step (sequence/ops.mojo:485-569, the product word and its
+    bias + activation follower, gemm/neural_dispatch.mojo:316-397): one whole-k chain per cell,
+    the follower fused into the product's store (one launch)."""
 
     def __init__(self, torch, D, x, w, bias, act):
         self.D, self.x, self.w, self.bias, self.act = D, x, w, bias, act
         self.out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
 
     def __call__(self, stream=None):
-        self.D.seq_gemm(self.x, self.w, self.out)
-        self.D.follow(self.out, self.D.EPI_BIAS_ACT, self.bias, self.act)
+        k = self.x.shape[1]
+        self.D.gemm_leaf_ptr(self.x, self.w, leaf=k, p_count=1, out=self.out, epi=self.D.EPI_BIAS_ACT,
+                             epi_p=self.bias, act=self.act)
 
 
 class _SeqAccumulate:

@@ -161,7 +161,8 @@ int mlg_gemm_leaf_ptr(float* c, const float* a, const float* b, int64_t m, int64
  * 4 BIAS_ACT ftz(act(ftz(ftz(cell) + ftz(epi_p[j])), epi_i)); 5 ACT_BWD
  * ftz(act_bwd(ftz(cell), ftz(epi_p[i n + j]), epi_i)).  Activation codes: 0 identity,
  * 1 logistic, 2 tanh, 3 relu, 4 softmax (left as is) (sequence/act_values.mojo:23-85).
- * epi_p must not overlap c. */
+ * The follower is fused into the product's store (one launch, as the reference fuses its
+ * GEMM_EPI_* kinds, gemm/checks/gemm_identical.mojo:9626-9671).  epi_p must not overlap c. */
 int mlg_gemm_leaf_ptr_epi(float* c, const float* a, const float* b, int64_t m, int64_t n, int64_t k, int64_t leaf,
                           int64_t p_count, int64_t a_si, int64_t a_sp, int64_t b_sp, int64_t b_sj, int32_t epi,
                           const float* epi_p, int32_t epi_i, void* stream);

@@ -87,4 +87,18 @@ __device__ __forceinline__ float act_bwd_value(float d, float z, int code) {
   return d;
 }
 
+// One follower on a stored cell `c` (already flushed): kind 3 PLUS_BIAS ftz(c + ftz(q)), 4 BIAS_ACT
+// act(ftz(c + ftz(q))), 5 ACT_BWD act_bwd(c, ftz(q)); the caller flushes the result and
+// canonicalizes NaNs (gemm/checks/gemm_identical.mojo:8884-8912).  Every input of every float
+// operation here is flushed on its integer word or cannot move the rounded result when the
+// kernel's mode flushes it (r * r in expf and x * x in tanhf, subnormal only for |r|, |x| below
+// 2^-62, where the fused multiply-add that reads them rounds to its addend either way), so the
+// value does not depend on the kernel's MODE.FP_DENORM.
+__device__ __forceinline__ float follow_one(float c, int kind, float q, int act) {
+  if (kind == EPI_PLUS_BIAS) return act_ftz(c + act_ftz(q));
+  if (kind == EPI_BIAS_ACT) return act_value(act_ftz(c + act_ftz(q)), act);
+  if (kind == EPI_ACT_BWD) return act_bwd_value(c, act_ftz(q), act);
+  return c;
+}
+
 }  // namespace mlg

@@ -644,10 +644,14 @@ int mlg_gemm_leaf_ptr_epi(float* c, const float* a, const float* b, int64_t m, i
     mlg::GemmProblem p{};
     view_layout(p, a_si, a_sp, b_sp, b_sj);
     p.c = c; p.a = a; p.b = b; p.m = m; p.n = n; p.k = k; p.leaf = leaf;
-    if (epi == mlg::EPI_PLUS_BIAS) p.bias = epi_p;
+    // the follower fused into the product's store (one launch, or the fold's when the leaves
+    // are split into groups)
+    if (epi == mlg::EPI_PLUS_BIAS) {
+      p.bias = epi_p;
+    } else {
+      p.epi = epi; p.epi_p = epi_p; p.act = epi_i;
+    }
     enqueue_gemm(p, (hipStream_t)stream);
-    if (epi != mlg::EPI_PLUS_BIAS)
-      hip_check(mlg::run_follow(c, n, m, n, 0, epi, epi_p, epi_i, (hipStream_t)stream), "follower launch");
   });
 }
 

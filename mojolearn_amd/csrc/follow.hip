@@ -18,13 +18,6 @@ constexpr int64_t FOLLOW_MAX_ROW_BLOCKS = 65535;
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-__device__ __forceinline__ float follow_one(float c, int kind, float q, int act) {
-  if (kind == EPI_PLUS_BIAS) return act_ftz(c + act_ftz(q));
-  if (kind == EPI_BIAS_ACT) return act_value(act_ftz(c + act_ftz(q)), act);
-  if (kind == EPI_ACT_BWD) return act_bwd_value(c, act_ftz(q), act);
-  return c;
-}
-
 // p: the bias (p[j], EPI_PLUS_BIAS / EPI_BIAS_ACT) or the forward values (p[i * n + j], EPI_ACT_BWD).
 template <bool VEC>
 __global__ void __launch_bounds__(FOLLOW_THREADS) follow_kernel(float* c, int64_t ldc, int64_t m, int64_t n,

@@ -1,4 +1,5 @@
 // gfx950 MFMA GEMM kernel of mojolearn.identical.gemm.fp32.v1 (any m, n, k; NN, NT, TN; f32, bf16, int8).
+#include "act.h"
 #include "device_common.h"
 #include "lds_stage.h"
 #include "mfma.h"
@@ -92,7 +93,25 @@ __device__ __forceinline__ void mfma_steps(v32f& acc, const char* la, const char
   }
 }
 
-template <int OP, int AT, int BT>
+// The tile of workgroup b among nb = tm x tn.  Workgroup b runs on XCD b % XCDS; the remap
+// gives XCD x a contiguous range of the tile sequence, in the order it dispatches them, and
+// the sequence walks bands of TILE_BAND row tiles column by column, so the 32 tiles an XCD runs
+// at once form a TILE_BAND x 8 block: the A row panels and B column panels they read are shared
+// in that XCD's L2 instead of fetched by every XCD.  A bijection of [0, nb): which tile a
+// workgroup computes never changes a cell's arithmetic.
+__device__ __forceinline__ int tile_of(int b, int nb, int tm, int tn) {
+  const int q = nb / XCDS, r = nb % XCDS;
+  const int x = b % XCDS, s = b / XCDS;
+  const int seq = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + s;
+  const int band = seq / (TILE_BAND * tn);
+  const int rows = tm - band * TILE_BAND < TILE_BAND ? tm - band * TILE_BAND : TILE_BAND;
+  const int local = seq - band * TILE_BAND * tn;
+  return (band * TILE_BAND + local % rows) * tn + local / rows;
+}
+
+// ACT: the store applies an activation follower (GemmArgs::epi 4 or 5; an instantiation of its
+// own, so the other products' kernels carry none of its code).
+template <int OP, int AT, int BT, bool ACT = false>
 __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   constexpr bool A_IMAJ = (OP != OP_TN);
   constexpr bool B_IMAJ = (OP == OP_NT);
@@ -111,7 +130,7 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   const int wr = wave >> 2;  // 0..1: rows wr*64 .. +63
   const int wc = wave & 3;   // 0..3: cols wc*32 .. +31
 
-  const int tile = blockIdx.x;
+  const int tile = tile_of(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n);
   const int64_t i0 = (int64_t)(tile / g.tiles_n) * BM;
   const int64_t j0 = (int64_t)(tile % g.tiles_n) * BN;
   const int64_t grp = blockIdx.y;
@@ -264,15 +283,30 @@ __global__ void __launch_bounds__(NTHREADS) gemm_mfma_kernel(GemmArgs g) {
   // acc holds the group root.  Element e -> block b = e/16, row (e%4) + 8*((e%16)/4) + 4*(lane/32) within it.
   const int64_t col = j0 + bcol;
   if (col < g.n) {
-    if (g.ngroups == 1) {
-      const float bj = g.bias ? g.bias[col] : 0.f;
+    if (ACT && g.ngroups == 1) {
+      // the activation followers: the root staged through this wave's fold slot (free now),
+      // then one cell at a time (a rolled loop: the activation's code once, not 32 times)
+      stk.put4(acc);
+      const float* staged = reinterpret_cast<const float*>(stk.s4);
+#pragma unroll 1
+      for (int e = 0; e < 32; ++e) {
+        const int blk = e >> 4, rr = e & 15;
+        const int64_t row = i0 + wr * 64 + 32 * blk + (rr & 3) + 8 * (rr >> 2) + 4 * (lane >> 5);
+        if (row < g.m) {
+          const float y = staged[(e >> 2) * 64 * 4 + (e & 3)];
+          const float q = g.epi == EPI_ACT_BWD ? g.epi_p[row * g.n + col] : g.epi_p[col];
+          g.c[row * g.ldc + col] = store_word(follow_one(act_ftz(y), g.epi, q, g.act));
+        }
+      }
+    } else if (g.ngroups == 1) {
+      const float bj = g.epi == EPI_PLUS_BIAS ? g.epi_p[col] : 0.f;
 #pragma unroll
       for (int e = 0; e < 32; ++e) {
         const int blk = e >> 4, rr = e & 15;
         const int64_t row = i0 + wr * 64 + 32 * blk + (rr & 3) + 8 * (rr >> 2) + 4 * (lane >> 5);
         if (row < g.m) {
           float y = acc[e];
-          if (g.bias) y = y + bj;  // ftz(C) + ftz(b) by the input flush
+          if (g.epi == EPI_PLUS_BIAS) y = y + bj;  // ftz(C) + ftz(b) by the input flush
           g.c[row * g.ldc + col] = store_word(y);
         }
       }
@@ -306,8 +340,8 @@ __global__ void repack_rows_kernel(char* dst, const char* src, int64_t rows, int
   }
 }
 
-__global__ void __launch_bounds__(256) fold_groups_kernel(float* c, int64_t ldc, const float* ws, const float* bias,
-                                                          int64_t m, int64_t n, int64_t ngroups) {
+__global__ void __launch_bounds__(256) fold_groups_kernel(float* c, int64_t ldc, const float* ws, int64_t m, int64_t n,
+                                                          int64_t ngroups, int epi, const float* epi_p, int act) {
   set_flush_inputs_mode();
   const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t cells = m * n;
@@ -320,18 +354,26 @@ __global__ void __launch_bounds__(256) fold_groups_kernel(float* c, int64_t ldc,
     y = stk.root(ws[t * cells + cell], (int)t);
   }
   const int64_t row = cell / n, col = cell - row * n;
-  if (bias) y = y + bias[col];
+  if (epi != EPI_NONE) {
+    const float q = epi == EPI_ACT_BWD ? epi_p[row * n + col] : epi_p[col];
+    y = follow_one(act_ftz(y), epi, q, act);
+  }
   c[row * ldc + col] = store_word(y);
 }
 
-template <int OP, int AT, int BT>
+template <int OP, int AT, int BT, bool ACT = false>
 static hipError_t launch_one(const GemmArgs& g, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((gemm_mfma_kernel<OP, AT, BT>), grid, dim3(NTHREADS), 0, stream, g);
+  hipLaunchKernelGGL((gemm_mfma_kernel<OP, AT, BT, ACT>), grid, dim3(NTHREADS), 0, stream, g);
   return hipGetLastError();
 }
 
 template <int OP>
 static hipError_t launch_types(const GemmArgs& g, int at, int bt, dim3 grid, hipStream_t s) {
+  if (g.epi >= EPI_BIAS_ACT && g.ngroups == 1) {
+    // the activation followers (the sequence word: float32 operands only)
+    if (at != T_F32 || bt != T_F32) return hipErrorInvalidValue;
+    return launch_one<OP, T_F32, T_F32, true>(g, grid, s);
+  }
   if (at == T_F32) {
     if (bt == T_F32) return launch_one<OP, T_F32, T_F32>(g, grid, s);
     if (bt == T_BF16) return launch_one<OP, T_F32, T_BF16>(g, grid, s);
@@ -355,11 +397,11 @@ hipError_t launch_repack(char* dst, const char* src, int64_t rows, int64_t cols,
   return hipGetLastError();
 }
 
-hipError_t launch_fold_groups(float* c, int64_t ldc, const float* ws, const float* bias, int64_t m, int64_t n,
-                              int64_t ngroups, hipStream_t stream) {
+hipError_t launch_fold_groups(float* c, int64_t ldc, const float* ws, int64_t m, int64_t n, int64_t ngroups, int epi,
+                              const float* epi_p, int act, hipStream_t stream) {
   const int64_t cells = m * n;
-  hipLaunchKernelGGL(fold_groups_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, stream, c, ldc, ws,
-                     bias, m, n, ngroups);
+  hipLaunchKernelGGL(fold_groups_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, stream, c, ldc, ws, m,
+                     n, ngroups, epi, epi_p, act);
   return hipGetLastError();
 }
 

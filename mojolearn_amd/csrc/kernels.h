@@ -26,6 +26,10 @@ struct GemmProblem {
   int seed;              // one leaf only: each chain starts from the flushed old C, not +0
   int seq;               // the caller's word (strides, seed): always the tile kernel
   int whole;             // one column range: never split into whole rounds + a grouped tail
+  // the activation followers fused into the store (act.h follow_one): 4 BIAS_ACT (epi_p[j]),
+  // 5 ACT_BWD (epi_p[i n + j]), with activation `act`; 0 none (the bias, if any, is `bias`)
+  int epi, act;
+  const float* epi_p;
 };
 
 // Workspace floats run_gemm needs for `p`: [completion counters][group roots][A repacked]

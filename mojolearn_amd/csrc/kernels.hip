@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <string>
 
+#include "act.h"
 #include "contract.h"
 #include "device_common.h"
 #include "gemv.h"
@@ -36,7 +37,7 @@ static int64_t gemv_cols(int bt, int op) { return op == OP_NT ? 64 : 64 * (4 / e
 // The skinny-M path takes OP_NN products with at most GV_MAXM float32 rows (dense operands,
 // chains from +0).
 static bool use_gemv(const GemmProblem& p) {
-  if (p.seq || p.a_type != T_F32 || p.m < 1 || p.m > GV_MAXM) return false;
+  if (p.seq || p.epi >= EPI_BIAS_ACT || p.a_type != T_F32 || p.m < 1 || p.m > GV_MAXM) return false;
   if (p.op == OP_NN) return true;
   // OP_NT: a lane's byte offset into a 64-row block of W is 32-bit
   return p.op == OP_NT && 64 * p.k * elem_bytes(p.b_type) + 512 < (int64_t(1) << 31);
@@ -188,9 +189,12 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
   const int64_t ldc = p.ldc > 0 ? p.ldc : p.n;
+  // the store's follower: the activation ones, or the bias
+  const int epi = p.epi >= EPI_BIAS_ACT ? p.epi : (p.bias ? EPI_PLUS_BIAS : EPI_NONE);
+  const float* epi_p = p.epi >= EPI_BIAS_ACT ? p.epi_p : p.bias;
   if (P == 0) {
     if (route) { *route |= ROUTE_ZERO_K; return hipSuccess; }
-    return launch_fold_groups(p.c, ldc, nullptr, p.bias, p.m, p.n, 0, stream);
+    return launch_fold_groups(p.c, ldc, nullptr, p.m, p.n, 0, epi, epi_p, p.act, stream);
   }
   if (use_gemv(p)) {
     GemvArgs v;
@@ -242,11 +246,13 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
   }
   GemmArgs g;
   g.c = p.c; g.a = p.a; g.b = p.b; g.scales = p.scales; g.bias = p.bias; g.ws = ws;
+  g.epi = epi; g.epi_p = epi_p; g.act = p.act;
   g.m = p.m; g.n = p.n; g.k = p.k; g.leaf = L; g.nleaves = P;
   g.ldc = ldc;
   g.seed = p.seed && P == 1 ? 1 : 0;
   if (p.seed && P != 1) return hipErrorInvalidValue;
   const int64_t tm = (p.m + BM - 1) / BM, tn = (p.n + BN - 1) / BN;
+  g.tiles_m = (int)tm;
   g.tiles_n = (int)tn;
   const int64_t gsz = P > 1 ? pick_group(P, tm * tn, num_cus) : 1;
   g.group = gsz;
@@ -290,7 +296,7 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
   dim3 grid((unsigned)(tm * tn), (unsigned)g.ngroups);
   hipError_t e = launch_mfma(g, p.op, p.a_type, p.b_type, grid, stream);
   if (e != hipSuccess || g.ngroups == 1) return e;
-  return launch_fold_groups(p.c, ldc, ws, p.bias, p.m, p.n, g.ngroups, stream);
+  return launch_fold_groups(p.c, ldc, ws, p.m, p.n, g.ngroups, epi, epi_p, p.act, stream);
 }
 
 // Zero `count` 32-bit words (the completion counters of a skinny product) with a kernel: a

@@ -35,10 +35,20 @@ struct GemmArgs {
   int64_t ngroups;
   int64_t a_pitch, b_pitch;  // stored row lengths in elements
   int64_t a_bytes, b_bytes;  // stored operand sizes
-  int tiles_n;
+  int tiles_m, tiles_n;
   int64_t ldc;        // C row stride
   int seed;           // one leaf: the chain starts from the old C cell
+  // the store's follower (act.h follow_one): 0 none, 3 PLUS_BIAS (epi_p[j]), 4 BIAS_ACT
+  // (epi_p[j], activation `act`), 5 ACT_BWD (epi_p[i n + j], activation `act`)
+  int epi, act;
+  const float* epi_p;
 };
+
+// XCDs of the device: workgroup b of a launch runs on XCD b % XCDS (round-robin dispatch).
+constexpr int XCDS = 8;
+// Row tiles walked together: an XCD's 32 concurrent tiles form a block of 4 row tiles x 8
+// column tiles, sharing A row panels and B column panels in its L2.
+constexpr int TILE_BAND = 4;
 
 // Launch gemm_mfma_kernel<op, a_type, b_type> on `grid` (tiles, leaf groups).
 hipError_t launch_mfma(const GemmArgs& g, int op, int a_type, int b_type, dim3 grid, hipStream_t stream);
@@ -48,8 +58,9 @@ hipError_t launch_mfma(const GemmArgs& g, int op, int a_type, int b_type, dim3 g
 hipError_t launch_repack(char* dst, const char* src, int64_t rows, int64_t cols, int64_t pitch, int eb,
                          int64_t s_r, int64_t s_c, hipStream_t stream);
 
-// Fold `ngroups` group roots ws[g][m][n] per cell (0 groups: store +0.0), add bias, store.
-hipError_t launch_fold_groups(float* c, int64_t ldc, const float* ws, const float* bias, int64_t m, int64_t n, int64_t ngroups,
-                              hipStream_t stream);
+// Fold `ngroups` group roots ws[g][m][n] per cell (0 groups: store +0.0), apply the store's
+// follower `epi` (as GemmArgs), store.
+hipError_t launch_fold_groups(float* c, int64_t ldc, const float* ws, int64_t m, int64_t n, int64_t ngroups,
+                              int epi, const float* epi_p, int act, hipStream_t stream);
 
 }  // namespace mlg

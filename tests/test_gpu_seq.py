@@ -199,3 +199,44 @@ def test_follower_layouts(oracle, layout, epi, act):
     oracle.epilogue(body, ldc, m, n, epi, p, act)
     want[off:] = body
     _same(tflat.cpu().numpy(), want, "buffer")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3, 4])
+def test_fused_activation_store_wide(oracle, act):
+    """Kind 4 fused into the product's store, on the wide value set: a one-step product
+    (A = the values, B = [1]) makes each cell its own flushed value, the bias -0.0 leaves it."""
+    rng = np.random.default_rng(60 + act)
+    x = _wide_values(rng, 1 << 20)
+    a = x.reshape(-1, 1).copy()
+    b = np.ones((1, 1), np.float32)
+    bias = np.full(1, -0.0, np.float32)
+    c = _dev().gemm_leaf_ptr(torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV), leaf=1, p_count=1, epi=4,
+                             epi_p=torch.from_numpy(bias).to(DEV), act=act)
+    torch.cuda.synchronize()
+    want = oracle.gemm(a, b, 0, leaf=1)
+    oracle.epilogue(want, 1, a.shape[0], 1, 4, bias, act)
+    _same(c.cpu().numpy(), want, f"fused activation {act}")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+def test_fused_derivative_store_wide(oracle, act):
+    rng = np.random.default_rng(70 + act)
+    d = _wide_values(rng, 1 << 18)
+    z = np.concatenate([np.array([0.0, -0.0, 1.0, -1.0, 0.5], np.float32),
+                        rng.uniform(-1, 1, d.size - 5).astype(np.float32)])
+    z[5:40] = d[:35]
+    a = d.reshape(-1, 1).copy()
+    b = np.ones((1, 1), np.float32)
+    c = _dev().gemm_leaf_ptr(torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV), leaf=1, p_count=1, epi=5,
+                             epi_p=torch.from_numpy(z).to(DEV), act=act)
+    torch.cuda.synchronize()
+    want = oracle.gemm(a, b, 0, leaf=1)
+    oracle.epilogue(want, 1, a.shape[0], 1, 5, z, act)
+    _same(c.cpu().numpy(), want, f"fused derivative {act}")
+
+
+def test_fused_store_is_one_launch():
+    """mlg_gemm_leaf_ptr_epi with an activation follower dispatches the product kernel alone
+    (no follower pass) when the leaves fold in one tile."""
+    from mojolearn_amd import device as D
+    assert D.route(2048, 4096, 4096, leaf=4096, num_cus=256) == {"tile"}
