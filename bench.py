@@ -192,6 +192,29 @@ def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=N
     return res
 
 
+def bench_read_floor(torch, steps, warmup, runs, nbuf=8):
+    """The memory floors of the decode GEMV's weight stream: a read-only pass over the same
+    rotating int8 W[4096x14336] buffers, (linear) in address order with 16-byte loads, and
+    (leaf) in the decode kernel's own order -- a wave per 128-row leaf and 256-byte strip, every
+    leaf of a column streamed at once, as the contract's leaf chains require."""
+    from mojolearn_amd import _native
+    L = _native.lib()
+    k, n = 4096, 14336
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(7)
+    bufs = [torch.randint(-127, 128, (k, n), dtype=torch.int8, device="cuda:0", generator=gen) for _ in range(nbuf)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    res = {}
+    for pattern, name in ((0, "linear"), (1, "leaf")):
+        calls = [lambda s, b=b, pattern=pattern: _native.check(
+            L.mlg_stream_read(b.data_ptr(), k, n, pattern, sink.data_ptr(), s.cuda_stream)) for b in bufs]
+        r = _timed(calls, max(steps, 2 * nbuf), warmup, torch, runs)
+        r.update({"us": r["ms"] * 1e3, "gbs": k * n / (r["ms"] * 1e-3) / 1e9,
+                  "hbm_frac": k * n / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes": k * n})
+        res[name] = r
+    return res
+
+
 def _repeat(fn, min_seconds, max_seconds):
     """Call fn until about `min_seconds` have passed; (calls, seconds, last result)."""
     reps, t0 = 0, time.perf_counter()
@@ -598,6 +621,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="time eager launches, no HIP graph")
     ap.add_argument("--compare", action="store_true",
                     help="also measure the rows the reference publishes for this path (MI325X)")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only time the read-only streams over the decode weight buffers and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (the byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -611,6 +636,9 @@ def main():
 
     if args.copy_calibration:
         copy_calibration(torch)
+        return
+    if args.read_floor:
+        print(json.dumps({"read_floor": bench_read_floor(torch, args.steps, args.warmup, runs=20)}), flush=True)
         return
     global EAGER
     EAGER = args.eager

@@ -720,10 +720,20 @@ int64_t mlg_gemm_route(const void* a, const void* b, int64_t m, int64_t n, int64
     const int cus = num_cus > 0 ? num_cus : num_cus_of_current_device();
     check_problem(p, cus);
     unsigned route = 0;
-    mlg::run_gemm(p, nullptr, cus, nullptr, &route);
+    hip_check(mlg::run_gemm(p, nullptr, cus, nullptr, &route), "gemm route");
     out = route;
   });
   return out;
+}
+
+// The memory floors of the skinny products, for bench.py (not part of the reference's
+// interface, so not in include/mlgemm.h).
+int mlg_stream_read(const void* w, int64_t rows, int64_t cols, int32_t pattern, uint32_t* sink, void* stream) {
+  return guarded([&] {
+    hip_check(mlg::run_stream_read(w, rows, cols, pattern, sink, static_cast<hipStream_t>(stream)),
+              "stream_read launch (pattern 0: 16-byte aligned, 16-byte multiple; pattern 1: rows a "
+              "multiple of 512, cols of 256)");
+  });
 }
 
 int mlg_gemm_ws(float* c, const void* a, const void* b, const float* scales, const float* bias,

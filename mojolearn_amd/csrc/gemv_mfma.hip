@@ -32,17 +32,14 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
   constexpr int NBLK = GV_CH / MF_RB;
   constexpr int RING = MF_AHEAD + 1;
   // lane l stages row l / 4, steps 32 * (l % 4) .. +31 (x + kb is 16-byte aligned: the host
-  // requires an aligned x and k a multiple of 128)
-  {
-    const int r = lane >> 2;
-    const f4* src = reinterpret_cast<const f4*>(xl + (int64_t)(r < m ? r : m - 1) * k + 32 * (lane & 3));
-    f4 v[8];
+  // requires an aligned x and k a multiple of 128).  The x loads go out first and the W ring's
+  // right after them; the LDS writes then wait for x alone (loads complete in order), so the
+  // weight stream is never held behind x's latency.
+  const int xr = lane >> 2;
+  const f4* src = reinterpret_cast<const f4*>(xl + (int64_t)(xr < m ? xr : m - 1) * k + 32 * (lane & 3));
+  f4 xv[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = src[c];
-    f4* dst = reinterpret_cast<f4*>(xs + r * GV_CH + 32 * (lane & 3));
-#pragma unroll
-    for (int c = 0; c < 8; ++c) dst[c] = v[c];
-  }
+  for (int c = 0; c < 8; ++c) xv[c] = src[c];
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
 
@@ -52,6 +49,11 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
 #pragma unroll
     for (int i = 0; i < MF_RB; ++i)
       ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * MF_RB + i) * rowbytes, 0);
+  {
+    f4* dst = reinterpret_cast<f4*>(xs + xr * GV_CH + 32 * (lane & 3));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) dst[c] = xv[c];
+  }
   // x[row][p .. p+3] for this lane's row (l % 16), four steps per LDS read
   const f4* xrow = reinterpret_cast<const f4*>(xs + (lane & 15) * GV_CH);
   f4 xc = xrow[0], xn;
@@ -158,13 +160,15 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
   constexpr int NBLK = GV_CH / MF_RB;
   constexpr int RING = MF_AHEAD + 1;
   // x rows 0 .. 4G-1 (rows past m repeat row m-1) by the leaf's 128 steps into xs[4G][GV_CH]:
-  // 32 f4 a row, 2G f4 a lane (x + kb is 16-byte aligned, k a multiple of 128)
+  // 32 f4 a row, 2G f4 a lane (x + kb is 16-byte aligned, k a multiple of 128).  As in the
+  // 16 x 16 kernel, x is requested first, the W ring right after, and the LDS writes wait for
+  // x alone.
+  f4 xv[2 * G];
 #pragma unroll
   for (int c = 0; c < 2 * G; ++c) {
     const int idx = lane + 64 * c;
     const int r = idx >> 5, q = idx & 31;
-    const f4 v = reinterpret_cast<const f4*>(xl + (int64_t)(r < m ? r : m - 1) * k)[q];
-    reinterpret_cast<f4*>(xs + r * GV_CH)[q] = v;
+    xv[c] = reinterpret_cast<const f4*>(xl + (int64_t)(r < m ? r : m - 1) * k)[q];
   }
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
@@ -174,6 +178,11 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
 #pragma unroll
     for (int i = 0; i < MF_RB; ++i)
       ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * MF_RB + i) * rowbytes, 0);
+#pragma unroll
+  for (int c = 0; c < 2 * G; ++c) {
+    const int idx = lane + 64 * c;
+    reinterpret_cast<f4*>(xs + (idx >> 5) * GV_CH)[idx & 31] = xv[c];
+  }
   const f4* xrow[G];
   f4 xc[G], xn[G];
 #pragma unroll

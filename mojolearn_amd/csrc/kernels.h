@@ -68,6 +68,10 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
 
 // Zero `count` words on `stream` with a kernel.
 hipError_t run_zero_words(unsigned int* p, int64_t count, hipStream_t stream);
+// Read-only streams over an int8 matrix W[rows][cols] (stream_read.hip): pattern 0 the whole
+// matrix in address order, pattern 1 the decode kernel's leaf-by-leaf reads.  Measurement only.
+hipError_t run_stream_read(const void* w, int64_t rows, int64_t cols, int pattern, uint32_t* sink,
+                           hipStream_t stream);
 
 // Elementwise conversions used by the low-bit surface (to_bf16 / from_bf16).
 hipError_t run_bf16_widen(float* out, const uint16_t* in, int64_t count, hipStream_t stream);

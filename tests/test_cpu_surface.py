@@ -28,6 +28,19 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(L, name), name
 
 
+def test_stream_read_refuses_before_any_launch():
+    """The read-floor entry (bench.py --read-floor) checks its shapes on the host: a missing
+    pointer, an unknown pattern, or a leaf pattern whose rows are not whole groups of four
+    128-row leaves is refused with a message and launches nothing."""
+    L = _native.lib()
+    sink = ctypes.c_uint32(0)
+    assert L.mlg_stream_read(None, 4096, 14336, 0, ctypes.addressof(sink), None) == 1
+    assert b"stream_read" in L.mlg_last_error()
+    buf = (ctypes.c_uint8 * 16)()
+    assert L.mlg_stream_read(ctypes.addressof(buf), 100, 256, 1, ctypes.addressof(sink), None) == 1
+    assert L.mlg_stream_read(ctypes.addressof(buf), 512, 256, 7, ctypes.addressof(sink), None) == 1
+
+
 def test_metadata_ops():
     assert _native.call(11, [], []) == 1
     assert _native.call(12, [], []) == 1

@@ -207,7 +207,10 @@ def test_bf16_conversions(oracle):
 
 
 GEMV_SHAPES = [(1, 1, 1), (1, 255, 129), (2, 256, 128), (7, 257, 1000), (16, 1000, 4096), (1, 4100, 300),
-               (3, 4096, 4097), (16, 33, 2048), (1, 14336, 4096), (2, 70, 140000), (5, 300, 515)]
+               (3, 4096, 4097), (16, 33, 2048), (1, 14336, 4096), (2, 70, 140000), (5, 300, 515),
+               # whole 128-row leaves at m <= 2: one partial group, two full groups and one leaf,
+               # three full groups and a partial one, sixteen groups
+               (2, 300, 640), (1, 1024, 1152), (1, 512, 1664), (2, 4096, 8192)]
 
 
 @pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
