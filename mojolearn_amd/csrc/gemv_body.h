@@ -301,6 +301,42 @@ __device__ __forceinline__ void gv_leaf_nt(float (&acc)[MR][1], const char* w, i
   }
 }
 
+// The completing workgroup's fold when the group count NG is a power of two (the decode shapes:
+// 32 leaves in groups of 8 or 4): the rest of the contract's tree is then complete -- adjacent
+// pairs, level by level -- and every root of up to 8 of this thread's cells is requested at once.
+template <int NG, int MR, int COLS, int THREADS, int CPT>
+__device__ __forceinline__ void gv_fold_pow2(const GemvArgs& g, int tid, int64_t cg, int m) {
+  constexpr int CB = CPT < 8 ? CPT : 8;
+#pragma unroll
+  for (int c0 = 0; c0 < CPT; c0 += CB) {
+    float v[CB][NG];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      const int cell = tid + (c0 + c) * THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
+#pragma unroll
+      for (int e = 0; e < NG; ++e)
+        v[c][e] = __hip_atomic_load(g.ws + (e * g.m + r) * g.n + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      const int cell = tid + (c0 + c) * THREADS;
+      const int r = cell / COLS, col = cell % COLS;
+      const int64_t j = cg * COLS + col;
+      if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
+#pragma unroll
+      for (int w = NG; w > 1; w /= 2)
+#pragma unroll
+        for (int q = 0; q < w / 2; ++q) v[c][q] = v[c][2 * q] + v[c][2 * q + 1];
+      float y = v[c][0];
+      if (g.bias) y = y + g.bias[j];
+      g.c[r * g.n + j] = store_word(y);
+    }
+  }
+}
+
 // The end of a skinny product, once every wave has written its leaf partial into
 // part[wave][row][col]: the workgroup's root (the tree over its up to GV_LEAVES leaves),
 // then either the store (one group) or the count and, in the workgroup that completes it,
@@ -394,7 +430,13 @@ __device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[LEAVE
   __syncthreads();
   if (!last_flag) return;
   const int64_t stride = g.m * g.n;
-  if (g.ngroups <= GV_FEW_GROUPS) {
+  if (g.ngroups == 2) {
+    gv_fold_pow2<2, MR, COLS, THREADS, CPT>(g, tid, cg, m);
+  } else if (g.ngroups == 4) {
+    gv_fold_pow2<4, MR, COLS, THREADS, CPT>(g, tid, cg, m);
+  } else if (g.ngroups == 8) {
+    gv_fold_pow2<8, MR, COLS, THREADS, CPT>(g, tid, cg, m);
+  } else if (g.ngroups <= GV_FEW_GROUPS) {
     // every root of up to 8 cells of this thread requested at once, then folded
     constexpr int CB = CPT < 8 ? CPT : 8;
 #pragma unroll

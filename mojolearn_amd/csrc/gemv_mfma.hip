@@ -54,9 +54,11 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
 #pragma unroll
     for (int c = 0; c < 8; ++c) dst[c] = xv[c];
   }
-  // x[row][p .. p+3] for this lane's row (l % 16), four steps per LDS read
+  // x[row][p .. p+3] for this lane's row (l % 16), four steps per LDS read, one read ahead in a
+  // two-entry buffer indexed by the (unrolled) group's parity, so no register is copied
   const f4* xrow = reinterpret_cast<const f4*>(xs + (lane & 15) * GV_CH);
-  f4 xc = xrow[0], xn;
+  f4 xb[2];
+  xb[0] = xrow[0];
 
 #pragma unroll
   for (int b = 0; b < NBLK; ++b) {
@@ -71,19 +73,19 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
 #pragma unroll
     for (int q0 = 0; q0 < MF_RB; q0 += 4) {
       const int s0 = b * MF_RB + q0;
-      if (s0 + 4 < GV_CH) xn = xrow[(s0 + 4) / 4];
+      const int xg = s0 / 4;
+      if (s0 + 4 < GV_CH) xb[(xg + 1) & 1] = xrow[xg + 1];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float wv[CPL];
         gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
-        const float xa = xc[q];
+        const float xa = xb[xg & 1][q];
 #pragma unroll
         for (int e = 0; e < CPL; ++e) {
           if (s0 + q == 0) acc[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(xa, wv[e], v16f{}, 0, 0, 0);
           else acc[e] = __builtin_amdgcn_mfma_f32_16x16x1f32(xa, wv[e], acc[e], 0, 0, 0);
         }
       }
-      if (s0 + 4 < GV_CH) xc = xn;
     }
   }
 }
@@ -184,11 +186,11 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
     reinterpret_cast<f4*>(xs + (idx >> 5) * GV_CH)[idx & 31] = xv[c];
   }
   const f4* xrow[G];
-  f4 xc[G], xn[G];
+  f4 xb[2][G];  // one read ahead, indexed by the (unrolled) group's parity: no register copies
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     xrow[g] = reinterpret_cast<const f4*>(xs + (4 * g + (lane & 3)) * GV_CH);
-    xc[g] = xrow[g][0];
+    xb[0][g] = xrow[g][0];
   }
 #pragma unroll
   for (int b = 0; b < NBLK; ++b) {
@@ -203,9 +205,10 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
 #pragma unroll
     for (int q0 = 0; q0 < MF_RB; q0 += 4) {
       const int s0 = b * MF_RB + q0;
+      const int xg = s0 / 4;
       if (s0 + 4 < GV_CH) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) xn[g] = xrow[g][(s0 + 4) / 4];
+        for (int g = 0; g < G; ++g) xb[(xg + 1) & 1][g] = xrow[g][xg + 1];
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -213,17 +216,13 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
         gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float xa = xc[g][q];
+          const float xa = xb[xg & 1][g][q];
 #pragma unroll
           for (int e = 0; e < CPL; ++e) {
             if (s0 + q == 0) acc[g][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(xa, wv[e], v4f{}, 0, 0, 0);
             else acc[g][e] = __builtin_amdgcn_mfma_f32_4x4x1f32(xa, wv[e], acc[g][e], 0, 0, 0);
           }
         }
-      }
-      if (s0 + 4 < GV_CH) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) xc[g] = xn[g];
       }
     }
   }
