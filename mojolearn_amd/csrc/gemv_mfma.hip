@@ -24,11 +24,27 @@ constexpr int GV_XS = 16 * GV_CH;  // floats of one wave's x block
 constexpr int MF_RB = 16;          // W rows per ring block
 constexpr int MF_AHEAD = 3;        // blocks requested ahead of the one being consumed
 
-template <int BT>
-__device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
+// The lane's CPL columns of one W row from its loaded bits u: bf16 widened exactly, int8
+// f32(code) * scale (one rounding; the scale flushed on input by MODE.FP_DENORM = 2).
+template <int BT, int CPL>
+__device__ __forceinline__ void mf_weights(uint32_t u, const float (&sc)[CPL], float (&wv)[CPL]) {
+  if constexpr (BT == T_F32) {
+    wv[0] = __uint_as_float(u);
+  } else if constexpr (BT == T_BF16) {
+    wv[0] = __uint_as_float(u << 16);
+    if constexpr (CPL > 1) wv[1] = __uint_as_float(u & 0xFFFF0000u);
+  } else {
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) wv[e] = (float)((int32_t)(u << (24 - 8 * e)) >> 24) * sc[e];
+  }
+}
+
+// CPL columns a lane: one 32-bit word of every W row, or (CPL * bytes == 2) one 16-bit half.
+template <int BT, int CPL>
+__device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[CPL], const char* wleaf, uint32_t loff,
                                              int rowbytes, const float* __restrict__ xl, int64_t k, int m,
-                                             float* xs, int lane, const float (&sc)[GvCols<BT>::cpl]) {
-  constexpr int CPL = GvCols<BT>::cpl;
+                                             float* xs, int lane, const float (&sc)[CPL]) {
+  constexpr bool HALF = CPL * Elem<BT>::bytes == 2;
   constexpr int NBLK = GV_CH / MF_RB;
   constexpr int RING = MF_AHEAD + 1;
   // lane l stages row l / 4, steps 32 * (l % 4) .. +31 (x + kb is 16-byte aligned: the host
@@ -44,11 +60,14 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
 
   uint32_t ring[RING][MF_RB];
+  auto load_row = [&](int row) -> uint32_t {
+    if constexpr (HALF) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)loff, row * rowbytes, 0);
+    else return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, row * rowbytes, 0);
+  };
 #pragma unroll
   for (int b = 0; b < MF_AHEAD; ++b)
 #pragma unroll
-    for (int i = 0; i < MF_RB; ++i)
-      ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * MF_RB + i) * rowbytes, 0);
+    for (int i = 0; i < MF_RB; ++i) ring[b][i] = load_row(b * MF_RB + i);
   {
     f4* dst = reinterpret_cast<f4*>(xs + xr * GV_CH + 32 * (lane & 3));
 #pragma unroll
@@ -65,9 +84,7 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
     if (b + MF_AHEAD < NBLK) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < MF_RB; ++i)
-        ring[(b + MF_AHEAD) % RING][i] =
-            __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ((b + MF_AHEAD) * MF_RB + i) * rowbytes, 0);
+      for (int i = 0; i < MF_RB; ++i) ring[(b + MF_AHEAD) % RING][i] = load_row((b + MF_AHEAD) * MF_RB + i);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -78,7 +95,7 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float wv[CPL];
-        gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
+        mf_weights<BT, CPL>(ring[b % RING][q0 + q], sc, wv);
         const float xa = xb[xg & 1][q];
 #pragma unroll
         for (int e = 0; e < CPL; ++e) {
@@ -90,11 +107,13 @@ __device__ __forceinline__ void gv_leaf_mfma(v16f (&acc)[GvCols<BT>::cpl], const
   }
 }
 
-template <int BT>
-__global__ void __launch_bounds__(MF_THREADS) gemv_mfma_nn_kernel(GemvArgs g, const float* __restrict__ x) {
+// CPL columns a lane (mf_cpl): with 16-bit lanes two workgroups share a CU (their leaf partials
+// and x blocks take 64 KB of LDS each, and the registers are held to four waves a SIMD).
+template <int BT, int CPL>
+__global__ void __launch_bounds__(MF_THREADS, CPL * Elem<BT>::bytes == 2 ? 2 : 1)
+gemv_mfma_nn_kernel(GemvArgs g, const float* __restrict__ x) {
   constexpr int MR = GV_MAXM;
-  constexpr int CPL = GvCols<BT>::cpl;
-  constexpr int COLS = GvCols<BT>::cols;
+  constexpr int COLS = 64 * CPL;
   constexpr int EB = Elem<BT>::bytes;
   // The waves' leaf partials; a wave's x block lives in its own partial area while it runs
   // its leaf when that area is large enough (int8, bf16), else in an area of its own (f32).
@@ -130,7 +149,7 @@ __global__ void __launch_bounds__(MF_THREADS) gemv_mfma_nn_kernel(GemvArgs g, co
     }
     const int64_t rowbytes = g.n * EB;
     const int64_t kb = t * GV_CH;
-    gv_leaf_mfma<BT>(acc, static_cast<const char*>(g.w) + kb * rowbytes, (uint32_t)(c0 * EB), (int)rowbytes,
+    gv_leaf_mfma<BT, CPL>(acc, static_cast<const char*>(g.w) + kb * rowbytes, (uint32_t)(c0 * EB), (int)rowbytes,
                      x + kb, g.k, m, XOWN > 0 ? &xown[wave][0] : &part[wave][0][0], lane, sc);
   }
 
@@ -297,9 +316,11 @@ hipError_t launch_gemv_mfma4_nn(const GemvArgs& g, const float* x, int b_type, i
 }
 
 hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, dim3 grid, hipStream_t stream) {
-  if (b_type == T_F32) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_F32>, grid, dim3(MF_THREADS), 0, stream, g, x);
-  else if (b_type == T_BF16) hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_BF16>, grid, dim3(MF_THREADS), 0, stream, g, x);
-  else hipLaunchKernelGGL(gemv_mfma_nn_kernel<T_I8>, grid, dim3(MF_THREADS), 0, stream, g, x);
+  if (b_type == T_F32)
+    hipLaunchKernelGGL((gemv_mfma_nn_kernel<T_F32, mf_cpl(T_F32)>), grid, dim3(MF_THREADS), 0, stream, g, x);
+  else if (b_type == T_BF16)
+    hipLaunchKernelGGL((gemv_mfma_nn_kernel<T_BF16, mf_cpl(T_BF16)>), grid, dim3(MF_THREADS), 0, stream, g, x);
+  else hipLaunchKernelGGL((gemv_mfma_nn_kernel<T_I8, mf_cpl(T_I8)>), grid, dim3(MF_THREADS), 0, stream, g, x);
   return hipGetLastError();
 }
 

@@ -33,6 +33,13 @@ static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
 
 static int64_t gemv_groups(int64_t P) { return (P + GV_LEAVES - 1) / GV_LEAVES; }
 static int64_t gemv_cols(int bt, int op) { return op == OP_NT ? 64 : 64 * (4 / elem_bytes(bt)); }
+// Columns of a column group of the 16 x 16 matrix-core kernel (OP_NN).
+static int64_t mf16_cols(int bt) { return 64 * mf_cpl(bt); }
+// The narrowest column group any skinny kernel of this weight type and op uses: the completion
+// counters a workspace carries cover it, whichever kernel the product's pointers then pick.
+static int64_t counter_cols(int bt, int op) {
+  return op == OP_NT ? gemv_cols(bt, op) : std::min(gemv_cols(bt, op), mf16_cols(bt));
+}
 
 // The skinny-M path takes OP_NN products with at most GV_MAXM float32 rows (dense operands,
 // chains from +0).
@@ -138,7 +145,7 @@ std::string launch_limit(const GemmProblem& p, int num_cus) {
   if (P < 1 || p.m <= 0 || p.n <= 0) return "";
   if (use_gemv(p)) {
     const int64_t groups = gemv_groups(P);
-    const int64_t ncg = (p.n + gemv_cols(p.b_type, p.op) - 1) / gemv_cols(p.b_type, p.op);
+    const int64_t ncg = (p.n + counter_cols(p.b_type, p.op) - 1) / counter_cols(p.b_type, p.op);
     if (groups > STACK_ROOTS)
       return "more leaf-group roots (" + std::to_string(groups) + ") than the fold stack covers (" +
              std::to_string(STACK_ROOTS) + "); use a larger leaf";
@@ -164,7 +171,7 @@ int64_t gemm_counter_count(const GemmProblem& p) {
   const int64_t L = p.leaf > 0 ? p.leaf : leaf_size(p.k);
   const int64_t P = leaf_count(p.k, L);
   if (!use_gemv(p) || p.m <= 0 || p.n <= 0 || gemv_groups(P) <= 1) return 0;
-  return (p.n + gemv_cols(p.b_type, p.op) - 1) / gemv_cols(p.b_type, p.op);
+  return (p.n + counter_cols(p.b_type, p.op) - 1) / counter_cols(p.b_type, p.op);
 }
 
 // Workspace: [completion counters][group roots][A repacked][B repacked], each part 256-byte
@@ -230,7 +237,8 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
                             dim3((unsigned)(v.ncg * v.ngroups)), stream);
     if (mfma) {
       // the matrix-core kernels: fewer, wider groups (at most the workspace sized for
-      // gemv_groups)
+      // gemv_groups); the 16 x 16 kernel's own column groups (at least counter_cols wide)
+      if (!four) v.ncg = (p.n + mf16_cols(p.b_type) - 1) / mf16_cols(p.b_type);
       const dim3 mgrid((unsigned)(v.ncg * v.ngroups));
       if (four) return launch_gemv_mfma4_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, mgrid, stream);
       return launch_gemv_mfma_nn(v, static_cast<const float*>(p.a), p.b_type, mgrid, stream);
