@@ -56,8 +56,8 @@ constexpr int MF4_LEAVES = 8;  // leaves per workgroup of the 4 x 4 kernel
 constexpr int MF4_THREADS = 64 * MF4_LEAVES;
 constexpr int MF_THREADS = 512;
 constexpr int MF_LEAVES = MF_THREADS / 64;
-// Columns a lane of the 16 x 16 kernel: int8 weights take 16-bit lanes (2 codes, 128-column
-// groups: twice the workgroups, four waves a SIMD); bf16 and f32 one 32-bit word.
+// Columns a lane of the matrix-core kernels: int8 weights take 16-bit lanes (2 codes, 128-column
+// groups: twice the workgroups, two a CU); bf16 and f32 one 32-bit word.
 constexpr int mf_cpl(int bt) { return bt == 2 ? 2 : (bt == 1 ? 2 : 1); }
 
 // vec (OP_NN): 0 element loads, 1 word (buffer) loads, 2 word loads of whole 128-row leaves.

@@ -173,11 +173,11 @@ gemv_mfma_nn_kernel(GemvArgs g, const float* __restrict__ x) {
 // below M = 4 (the 16 x 16 shape computes 16).
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <int BT, int G>
-__device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
-                                              int rowbytes, const float* __restrict__ xl, int64_t k, int m, float* xs,
-                                              int lane, const float (&sc)[GvCols<BT>::cpl]) {
-  constexpr int CPL = GvCols<BT>::cpl;
+template <int BT, int G, int CPL>
+__device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][CPL], const char* wleaf, uint32_t loff, int rowbytes,
+                                              const float* __restrict__ xl, int64_t k, int m, float* xs, int lane,
+                                              const float (&sc)[CPL]) {
+  constexpr bool HALF = CPL * Elem<BT>::bytes == 2;
   constexpr int NBLK = GV_CH / MF_RB;
   constexpr int RING = MF_AHEAD + 1;
   // x rows 0 .. 4G-1 (rows past m repeat row m-1) by the leaf's 128 steps into xs[4G][GV_CH]:
@@ -193,12 +193,15 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
   }
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf), (short)0, 0x7FFFFFFF, RSRC_WORD3);
+  auto load_row = [&](int row) -> uint32_t {
+    if constexpr (HALF) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)loff, row * rowbytes, 0);
+    else return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, row * rowbytes, 0);
+  };
   uint32_t ring[RING][MF_RB];
 #pragma unroll
   for (int b = 0; b < MF_AHEAD; ++b)
 #pragma unroll
-    for (int i = 0; i < MF_RB; ++i)
-      ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, (b * MF_RB + i) * rowbytes, 0);
+    for (int i = 0; i < MF_RB; ++i) ring[b][i] = load_row(b * MF_RB + i);
 #pragma unroll
   for (int c = 0; c < 2 * G; ++c) {
     const int idx = lane + 64 * c;
@@ -216,9 +219,7 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
     if (b + MF_AHEAD < NBLK) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < MF_RB; ++i)
-        ring[(b + MF_AHEAD) % RING][i] =
-            __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, ((b + MF_AHEAD) * MF_RB + i) * rowbytes, 0);
+      for (int i = 0; i < MF_RB; ++i) ring[(b + MF_AHEAD) % RING][i] = load_row((b + MF_AHEAD) * MF_RB + i);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -232,7 +233,7 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float wv[CPL];
-        gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
+        mf_weights<BT, CPL>(ring[b % RING][q0 + q], sc, wv);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float xa = xb[xg & 1][g][q];
@@ -247,11 +248,12 @@ __device__ __forceinline__ void gv_leaf_mfma4(v4f (&acc)[G][GvCols<BT>::cpl], co
   }
 }
 
-template <int BT, int G>
-__global__ void __launch_bounds__(MF4_THREADS) gemv_mfma4_nn_kernel(GemvArgs g, const float* __restrict__ x) {
+// CPL columns a lane (mf_cpl), as in the 16 x 16 kernel.
+template <int BT, int G, int CPL>
+__global__ void __launch_bounds__(MF4_THREADS, CPL * Elem<BT>::bytes == 2 ? 2 : 1)
+gemv_mfma4_nn_kernel(GemvArgs g, const float* __restrict__ x) {
   constexpr int MR = 4 * G;
-  constexpr int CPL = GvCols<BT>::cpl;
-  constexpr int COLS = GvCols<BT>::cols;
+  constexpr int COLS = 64 * CPL;
   constexpr int EB = Elem<BT>::bytes;
   constexpr int XS = MR * GV_CH;  // floats of one wave's x block
   __shared__ __attribute__((aligned(16))) float part[MF4_LEAVES][MR][COLS];
@@ -286,8 +288,8 @@ __global__ void __launch_bounds__(MF4_THREADS) gemv_mfma4_nn_kernel(GemvArgs g, 
     }
     const int64_t rowbytes = g.n * EB;
     const int64_t kb = t * GV_CH;
-    gv_leaf_mfma4<BT, G>(acc, static_cast<const char*>(g.w) + kb * rowbytes, (uint32_t)(c0 * EB), (int)rowbytes,
-                         x + kb, g.k, m, &xown[wave][0], lane, sc);
+    gv_leaf_mfma4<BT, G, CPL>(acc, static_cast<const char*>(g.w) + kb * rowbytes, (uint32_t)(c0 * EB),
+                              (int)rowbytes, x + kb, g.k, m, &xown[wave][0], lane, sc);
   }
 
   // lane l: rows 4 gg + r of column CPL l + e in acc[gg][e][r]
@@ -303,10 +305,10 @@ __global__ void __launch_bounds__(MF4_THREADS) gemv_mfma4_nn_kernel(GemvArgs g, 
 hipError_t launch_gemv_mfma4_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, dim3 grid,
                                 hipStream_t stream) {
   const bool two = m > 4;
-#define MLG_MF4(BT)                                                                                          \
-  do {                                                                                                       \
-    if (two) hipLaunchKernelGGL((gemv_mfma4_nn_kernel<BT, 2>), grid, dim3(MF4_THREADS), 0, stream, g, x);    \
-    else hipLaunchKernelGGL((gemv_mfma4_nn_kernel<BT, 1>), grid, dim3(MF4_THREADS), 0, stream, g, x);        \
+#define MLG_MF4(BT)                                                                                               \
+  do {                                                                                                            \
+    if (two) hipLaunchKernelGGL((gemv_mfma4_nn_kernel<BT, 2, mf_cpl(BT)>), grid, dim3(MF4_THREADS), 0, stream, g, x); \
+    else hipLaunchKernelGGL((gemv_mfma4_nn_kernel<BT, 1, mf_cpl(BT)>), grid, dim3(MF4_THREADS), 0, stream, g, x);     \
   } while (0)
   if (b_type == T_F32) MLG_MF4(T_F32);
   else if (b_type == T_BF16) MLG_MF4(T_BF16);

@@ -33,7 +33,7 @@ static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
 
 static int64_t gemv_groups(int64_t P) { return (P + GV_LEAVES - 1) / GV_LEAVES; }
 static int64_t gemv_cols(int bt, int op) { return op == OP_NT ? 64 : 64 * (4 / elem_bytes(bt)); }
-// Columns of a column group of the 16 x 16 matrix-core kernel (OP_NN).
+// Columns of a column group of the matrix-core kernels (OP_NN, 4 x 4 and 16 x 16 shapes).
 static int64_t mf16_cols(int bt) { return 64 * mf_cpl(bt); }
 // The narrowest column group any skinny kernel of this weight type and op uses: the completion
 // counters a workspace carries cover it, whichever kernel the product's pointers then pick.
@@ -237,8 +237,8 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
                             dim3((unsigned)(v.ncg * v.ngroups)), stream);
     if (mfma) {
       // the matrix-core kernels: fewer, wider groups (at most the workspace sized for
-      // gemv_groups); the 16 x 16 kernel's own column groups (at least counter_cols wide)
-      if (!four) v.ncg = (p.n + mf16_cols(p.b_type) - 1) / mf16_cols(p.b_type);
+      // gemv_groups) and their own column groups (at least counter_cols wide)
+      v.ncg = (p.n + mf16_cols(p.b_type) - 1) / mf16_cols(p.b_type);
       const dim3 mgrid((unsigned)(v.ncg * v.ngroups));
       if (four) return launch_gemv_mfma4_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, mgrid, stream);
       return launch_gemv_mfma_nn(v, static_cast<const float*>(p.a), p.b_type, mgrid, stream);
