@@ -5,6 +5,17 @@
 
 namespace mlg {
 
+// The arguments the first W loads depend on, named by an empty asm at a matrix-core skinny
+// kernel's start: both lines of the argument block are then fetched in one round trip, not in
+// dependent pieces around the workgroup index split and the leaf check (measured: M = 16
+// decode 1.7% faster).  The asm is volatile, so the compiler can no longer prove memory
+// unchanged since the kernel's start: a kernel that reads x with scalar loads (gemv_nn) would
+// read it with vector loads after it, and does without it.
+__device__ __forceinline__ void gv_fetch_args(const GemvArgs& g, const float* x) {
+  __asm__ volatile("" ::"s"(g.w), "s"(g.scales), "s"(g.m), "s"(g.n), "s"(g.k), "s"(g.leaf), "s"(g.nleaves),
+                   "s"(g.ncg), "s"(x));
+}
+
 // The contract's tree over a cell's P roots base[t * stride], read with agent-scope atomic
 // loads issued up to GV_FOLD_BATCH at a time.
 __device__ __forceinline__ float fold_roots(const float* base, int64_t P, int64_t stride) {
@@ -130,12 +141,13 @@ __device__ __forceinline__ void gv_steps(float (&acc)[MR][GvCols<BT>::cpl], cons
 // the rows travel in blocks of GV_RB through a ring of GV_AHEAD + 1 register blocks, GV_AHEAD
 // blocks requested ahead of the one being consumed, so the wave keeps loads in flight while
 // it computes on the rows that have landed.  x is read XB steps at a time, one batch ahead.
-// `wleaf` is the leaf's first row; rows are `rowbytes` apart (GV_CH * rowbytes < 2^31).
+// `wleaf` is the leaf's first row; rows are `rowbytes` apart (GV_CH * rowbytes < 2^31).  A
+// lane's word is 32 bits, or 16 (two int8 codes) where GvCols<BT, false, true> says so.
 constexpr int GV_RB = 16;
 constexpr int GV_AHEAD = 3;
 
-template <int BT>
-__device__ __forceinline__ void gv_weights(uint32_t u, const float (&sc)[GvCols<BT>::cpl], float (&wv)[GvCols<BT>::cpl]) {
+template <int BT, int CPL>
+__device__ __forceinline__ void gv_weights(uint32_t u, const float (&sc)[CPL], float (&wv)[CPL]) {
   if constexpr (BT == T_F32) {
     wv[0] = __uint_as_float(u);
   } else if constexpr (BT == T_BF16) {
@@ -143,15 +155,16 @@ __device__ __forceinline__ void gv_weights(uint32_t u, const float (&sc)[GvCols<
     wv[1] = __uint_as_float(u & 0xFFFF0000u);
   } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) wv[e] = (float)((int32_t)(u << (24 - 8 * e)) >> 24) * sc[e];
+    for (int e = 0; e < CPL; ++e) wv[e] = (float)((int32_t)(u << (24 - 8 * e)) >> 24) * sc[e];
   }
 }
 
-template <int BT, int MR>
-__device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], const char* wleaf, uint32_t loff,
-                                             int rowbytes, const float* __restrict__ xl, int64_t k, int m,
-                                             const float (&sc)[GvCols<BT>::cpl]) {
-  constexpr int CPL = GvCols<BT>::cpl;
+template <int BT, int MR, int CPL>
+__device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][CPL], const char* wleaf, uint32_t loff, int rowbytes,
+                                             const float* __restrict__ xl, int64_t k, int m,
+                                             const float (&sc)[CPL]) {
+  static_assert(CPL == GvCols<BT, false, true>::cpl, "a whole-leaf lane's columns");
+  constexpr bool HALF = CPL * Elem<BT>::bytes == 2;  // 16-bit words
   constexpr int NBLK = GV_CH / GV_RB;
   constexpr int RING = GV_AHEAD + 1;
   constexpr int XB = MR <= 16 ? 16 / MR : 1;  // 16 x values a batch: two batches fit the scalar file
@@ -160,6 +173,10 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], 
   auto block_rs = [&](int b) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf) + (int64_t)b * GV_RB * rowbytes, (short)0,
                                              0x7FFFFFFF, RSRC_WORD3);
+  };
+  auto load_word = [&](__amdgpu_buffer_rsrc_t rs, int soff) -> uint32_t {
+    if constexpr (HALF) return __builtin_amdgcn_raw_buffer_load_b16(rs, (int)loff, soff, 0);
+    else return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, soff, 0);
   };
   const float* xr[MR];
 #pragma unroll
@@ -174,7 +191,7 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], 
     // blocks (held, they overflow the scalar file next to x).
     if constexpr (MR > 1) __asm__ volatile("" : "+s"(rb));
 #pragma unroll
-    for (int i = 0; i < GV_RB; ++i) ring[b][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, i * rb, 0);
+    for (int i = 0; i < GV_RB; ++i) ring[b][i] = load_word(rs, i * rb);
   }
   float xc[MR][XB], xn[MR][XB];
 #pragma unroll
@@ -190,8 +207,7 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], 
       int rb = rowbytes;
       if constexpr (MR > 1) __asm__ volatile("" : "+s"(rb));
 #pragma unroll
-      for (int i = 0; i < GV_RB; ++i)
-        ring[(b + GV_AHEAD) % RING][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, i * rb, 0);
+      for (int i = 0; i < GV_RB; ++i) ring[(b + GV_AHEAD) % RING][i] = load_word(rs, i * rb);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -206,7 +222,7 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][GvCols<BT>::cpl], 
 #pragma unroll
       for (int q = 0; q < XB; ++q) {
         float wv[CPL];
-        gv_weights<BT>(ring[b % RING][q0 + q], sc, wv);
+        gv_weights<BT, CPL>(ring[b % RING][q0 + q], sc, wv);
 #pragma unroll
         for (int r = 0; r < MR; ++r)
 #pragma unroll
@@ -338,7 +354,7 @@ __device__ __forceinline__ void gv_fold_pow2(const GemvArgs& g, int tid, int64_t
 }
 
 // The end of a skinny product, once every wave has written its leaf partial into
-// part[wave][row][col]: the workgroup's root (the tree over its up to GV_LEAVES leaves),
+// part[wave][row][col]: the workgroup's root (the tree over its up to LEAVES leaves),
 // then either the store (one group) or the count and, in the workgroup that completes it,
 // the fold of every group's root (the rest of the contract's tree), bias and store.
 template <int MR, int COLS, int LEAVES = GV_LEAVES, int THREADS = GV_THREADS>
@@ -487,13 +503,16 @@ __device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[LEAVE
   if (tid == 0) __hip_atomic_store(&g.counter[cg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One skinny product: OP_NN (W[k][n], FULLLEAF: every leaf exactly 128 rows) or OP_NT (W[n][k]).
-template <int BT, int MR, bool VEC, bool FULLLEAF, bool NT>
-__device__ __forceinline__ void gemv_body(const GemvArgs& g, const float* __restrict__ x) {
-  constexpr int CPL = GvCols<BT, NT>::cpl;
-  constexpr int COLS = GvCols<BT, NT>::cols;
+// One skinny product: OP_NN (W[k][n], FULLLEAF: every leaf exactly 128 rows) or OP_NT (W[n][k]),
+// LEAVES leaves (waves) a workgroup.  The argument block is taken by value: the compiler then
+// requests both of its cache lines before the workgroup index split (measured 1-2% at M <= 2).
+template <int BT, int MR, bool VEC, bool FULLLEAF, bool NT, int LEAVES = GV_LEAVES>
+__device__ __forceinline__ void gemv_body(GemvArgs g, const float* __restrict__ x) {
+  constexpr int CPL = GvCols<BT, NT, FULLLEAF>::cpl;
+  constexpr int COLS = GvCols<BT, NT, FULLLEAF>::cols;
   constexpr int EB = Elem<BT>::bytes;
-  __shared__ float part[GV_LEAVES][MR][COLS];
+  static_assert(LEAVES == GV_LEAVES || (FULLLEAF && !NT), "wide workgroups take whole leaves");
+  __shared__ float part[LEAVES][MR][COLS];
   __shared__ unsigned int last_flag;
 
   set_flush_inputs_mode();
@@ -501,9 +520,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, const float* __rest
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: leaf and k range too
-  const int64_t cg = blockIdx.x % g.ncg;
-  const int64_t grp = blockIdx.x / g.ncg;
-  const int64_t t = grp * GV_LEAVES + wave;  // this wave's leaf
+  // the grid holds at most INT32_MAX workgroups (the host refuses more): a 32-bit split
+  const int64_t cg = blockIdx.x % (uint32_t)g.ncg;
+  const int64_t grp = blockIdx.x / (uint32_t)g.ncg;
+  const int64_t t = grp * LEAVES + wave;  // this wave's leaf
   const int m = (int)g.m;
 
   float acc[MR][CPL];
@@ -562,12 +582,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& g, const float* __rest
     }
   }
 
-  // The group's root: the tree over its (up to GV_LEAVES) leaf partials, through LDS.
+  // The group's root: the tree over its (up to LEAVES) leaf partials, through LDS.
 #pragma unroll
   for (int r = 0; r < MR; ++r)
 #pragma unroll
     for (int e = 0; e < CPL; ++e) part[wave][r][lane * CPL + e] = acc[r][e];
-  gv_finish<MR, COLS>(g, part, last_flag, tid, grp, cg, m);
+  gv_finish<MR, COLS, LEAVES, 64 * LEAVES>(g, part, last_flag, tid, grp, cg, m);
 }
 
 }  // namespace mlg

@@ -124,12 +124,14 @@ gemv_mfma_nn_kernel(GemvArgs g, const float* __restrict__ x) {
   __shared__ unsigned int last_flag;
 
   set_flush_inputs_mode();
+  gv_fetch_args(g, x);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t cg = blockIdx.x % g.ncg;
-  const int64_t grp = blockIdx.x / g.ncg;
+  // the grid holds at most INT32_MAX workgroups (the host refuses more): a 32-bit split
+  const int64_t cg = blockIdx.x % (uint32_t)g.ncg;
+  const int64_t grp = blockIdx.x / (uint32_t)g.ncg;
   const int64_t t = grp * MF_LEAVES + wave;  // this wave's leaf
   const int m = (int)g.m;
 
@@ -261,12 +263,14 @@ gemv_mfma4_nn_kernel(GemvArgs g, const float* __restrict__ x) {
   __shared__ unsigned int last_flag;
 
   set_flush_inputs_mode();
+  gv_fetch_args(g, x);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t cg = blockIdx.x % g.ncg;
-  const int64_t grp = blockIdx.x / g.ncg;
+  // the grid holds at most INT32_MAX workgroups (the host refuses more): a 32-bit split
+  const int64_t cg = blockIdx.x % (uint32_t)g.ncg;
+  const int64_t grp = blockIdx.x / (uint32_t)g.ncg;
   const int64_t t = grp * MF4_LEAVES + wave;  // this wave's leaf
   const int m = (int)g.m;
 

@@ -32,13 +32,14 @@ static int pick_group(int64_t nleaves, int64_t tiles, int num_cus) {
 }
 
 static int64_t gemv_groups(int64_t P) { return (P + GV_LEAVES - 1) / GV_LEAVES; }
-static int64_t gemv_cols(int bt, int op) { return op == OP_NT ? 64 : 64 * (4 / elem_bytes(bt)); }
+static int64_t gemv_cols(int bt, int op, bool full = false) { return 64 * gv_cpl(bt, op == OP_NT, full); }
 // Columns of a column group of the matrix-core kernels (OP_NN, 4 x 4 and 16 x 16 shapes).
 static int64_t mf16_cols(int bt) { return 64 * mf_cpl(bt); }
 // The narrowest column group any skinny kernel of this weight type and op uses: the completion
 // counters a workspace carries cover it, whichever kernel the product's pointers then pick.
 static int64_t counter_cols(int bt, int op) {
-  return op == OP_NT ? gemv_cols(bt, op) : std::min(gemv_cols(bt, op), mf16_cols(bt));
+  return op == OP_NT ? gemv_cols(bt, op)
+                     : std::min({gemv_cols(bt, op), gemv_cols(bt, op, true), mf16_cols(bt)});
 }
 
 // The skinny-M path takes OP_NN products with at most GV_MAXM float32 rows (dense operands,
@@ -226,6 +227,17 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
                       16 * p.k * 4 < (int64_t(1) << 31);
     const bool four = p.m <= GV_MFMA4_MAX_M;
     if (mfma) v.ngroups = (P + (four ? MF4_LEAVES : MF_LEAVES) - 1) / (four ? MF4_LEAVES : MF_LEAVES);
+    // whole leaves (vec 2): int8 on 16-bit lanes, and for the decode rows (m <= 2) eight leaves
+    // a workgroup when that still leaves a workgroup for every CU
+    int leaves = GV_LEAVES;
+    if (p.op == OP_NN && !mfma && vec == 2) {
+      v.ncg = (p.n + gemv_cols(p.b_type, p.op, true) - 1) / gemv_cols(p.b_type, p.op, true);
+      const int64_t wide = (P + GV_WIDE_LEAVES - 1) / GV_WIDE_LEAVES;
+      if (p.m <= 2 && v.ncg * wide >= num_cus) {
+        leaves = GV_WIDE_LEAVES;
+        v.ngroups = wide;
+      }
+    }
     if (route) {
       *route |= p.op == OP_NT ? ROUTE_GEMV_NT : (mfma ? (four ? ROUTE_MFMA4 : ROUTE_MFMA16) : ROUTE_GEMV_NN);
       if (v.ngroups > 1) *route |= ROUTE_GEMV_GROUPS;
@@ -243,8 +255,8 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
       if (four) return launch_gemv_mfma4_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, mgrid, stream);
       return launch_gemv_mfma_nn(v, static_cast<const float*>(p.a), p.b_type, mgrid, stream);
     }
-    return launch_gemv_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, vec, dim3((unsigned)(v.ncg * v.ngroups)),
-                          stream);
+    return launch_gemv_nn(v, static_cast<const float*>(p.a), p.b_type, p.m, vec, leaves,
+                          dim3((unsigned)(v.ncg * v.ngroups)), stream);
   }
   GemmProblem p1, p2;
   if (tail_split(p, P, num_cus, p1, p2)) {

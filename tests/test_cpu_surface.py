@@ -226,6 +226,10 @@ def test_route_names_the_kernels_without_a_device():
     assert R(16, 14336, 4096, b_type=D.T_I8) == {"mfma16", "gemv_groups"}
     assert R(1, 14336, 4096, op=D.OP_NT) == {"gemv_nt", "gemv_groups"}
     assert R(1, 64, 128) == {"gemv_nn"}  # one leaf group: no cross-workgroup fold
+    # whole leaves at m <= 2 take eight leaves a workgroup while the launch keeps a workgroup
+    # for every CU: int8 n = 32768 is 256 column groups of 128, k = 1024 is 8 leaves
+    assert R(1, 32768, 1024, b_type=D.T_I8) == {"gemv_nn"}
+    assert D.route(1, 32768, 1024, b_type=D.T_I8, num_cus=512) == {"gemv_nn", "gemv_groups"}
     assert R(3, 5, 0) == {"zero_k"}
     assert R(16, 64, 4096, a=4) == {"gemv_nn", "gemv_groups"}  # x off the 16-byte grid: the VALU kernel
     assert "repack" in R(64, 64, 100, a=4)

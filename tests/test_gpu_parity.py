@@ -209,16 +209,18 @@ def test_bf16_conversions(oracle):
 GEMV_SHAPES = [(1, 1, 1), (1, 255, 129), (2, 256, 128), (7, 257, 1000), (16, 1000, 4096), (1, 4100, 300),
                (3, 4096, 4097), (16, 33, 2048), (1, 14336, 4096), (2, 70, 140000), (5, 300, 515),
                # whole 128-row leaves at m <= 2: one partial group, two full groups and one leaf,
-               # three full groups and a partial one, sixteen groups
-               (2, 300, 640), (1, 1024, 1152), (1, 512, 1664), (2, 4096, 8192)]
+               # three full groups and a partial one, sixteen groups (eight of eight leaves at
+               # 256 CUs); eight-leaf groups with a ragged last group and column group
+               (2, 300, 640), (1, 1024, 1152), (1, 512, 1664), (2, 4096, 8192), (1, 8196, 4480),
+               (2, 8196, 4480)]
 
 
 @pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
 @pytest.mark.parametrize("shape", GEMV_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_SHAPES])
 def test_skinny_m(oracle, shape, wt):
     """The skinny-M (decode GEMV) path: a leaf per wave streamed into registers (word loads,
-    or element loads when a row is not a multiple of 4 bytes), groups of 4 leaves folded in
-    LDS, the last-arriving group folding the rest; leaves longer than 128 rows (k > 131072),
+    or element loads when a row is not a multiple of 4 bytes), groups of 4 leaves (8 with
+    whole leaves at m <= 2 on a wide launch) folded in LDS, the last-arriving group folding the rest; leaves longer than 128 rows (k > 131072),
     ragged last leaves, ragged last groups."""
     D = _dev()
     m, n, k = shape
