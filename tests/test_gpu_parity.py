@@ -258,6 +258,53 @@ GEMV_MFMA_SHAPES = [(5, 257, 1024), (8, 300, 4096), (12, 64, 512), (16, 1024, 12
                     (3, 257, 4096), (4, 14336, 4096), (6, 129, 1152), (4, 64, 640)]
 
 
+# whole 128-row leaves with 3 <= m <= 16 and x off the 16-byte grid: the VALU kernel's straight-line
+# leaf with 4, 8 and 16 rows of chains (int8 on 16-bit lanes), which aligned x never reaches
+GEMV_OFFGRID_SHAPES = [(3, 300, 1024), (4, 257, 640), (8, 1000, 4096), (16, 129, 1152), (16, 2048, 4096)]
+
+
+@pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
+@pytest.mark.parametrize("shape", GEMV_OFFGRID_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_OFFGRID_SHAPES])
+def test_skinny_m_x_off_grid(oracle, shape, wt):
+    """x starting one float into its buffer (4-byte but not 16-byte aligned) keeps a whole-leaf
+    product with 3 <= m <= 16 off the matrix-core kernels: gemv_nn_kernel's whole-leaf variant
+    runs its 4-, 8- or 16-row chains, on poisoned outputs with the fused bias."""
+    from mojolearn_amd import device as D
+    m, n, k = shape
+    rng = np.random.default_rng(m * 7 + n + k)
+    x = _values(rng, (m, k), "wide")
+    bias = _values(rng, (n,), "wide")
+    print(f"skinny off-grid x {wt} m={m} n={n} k={k}", flush=True)
+    buf = torch.empty(m * k + 4, dtype=torch.float32, device=DEV)
+    tx = buf[1:1 + m * k].view(m, k)
+    tx.copy_(torch.from_numpy(x))
+    assert tx.data_ptr() % 16 != 0
+    tbias = torch.from_numpy(bias).to(DEV)
+    out = torch.full((m, n), POISON, dtype=torch.float32, device=DEV)
+    if wt == "f32":
+        w = _values(rng, (k, n), "wide")
+        tw = torch.from_numpy(w).to(DEV)
+        D.gemm(tx, tw, bias=tbias, out=out)
+        want = oracle.gemm_fast(x, w, 0)
+        bt = D.T_F32
+    elif wt == "bf16":
+        wb = oracle.bf16_narrow(_values(rng, (k, n), "wide"))
+        tw = torch.from_numpy(wb.view(np.int16)).to(DEV)
+        D.gemm_bf16w(tx, tw, bias=tbias, out=out)
+        want = oracle.gemm_fast(x, oracle.bf16_widen(wb), 0)
+        bt = D.T_BF16
+    else:
+        codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        tw = torch.from_numpy(codes).to(DEV)
+        D.gemm_int8w(tx, tw, torch.from_numpy(scales).to(DEV), bias=tbias, out=out)
+        want = oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0)
+        bt = D.T_I8
+    torch.cuda.synchronize()
+    assert "gemv_nn" in D.route(m, n, k, b_type=bt, a=tx, b=tw)
+    assert_bits(out.cpu().numpy(), oracle.nan_canon(oracle.bias(want, bias)), f"skinny off-grid {wt} {shape}")
+
+
 @pytest.mark.parametrize("kind", ["wide", "special"])
 @pytest.mark.parametrize("wt", ["f32", "bf16", "i8"])
 @pytest.mark.parametrize("shape", GEMV_MFMA_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in GEMV_MFMA_SHAPES])
