@@ -160,11 +160,13 @@ def bench_product(torch, D, a, b, steps, warmup, want_fn=None, runs=1):
     return res
 
 
-def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=None, wdeq=None):
+def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=None, wdeq=None, packed=False):
     """int8-weight GEMV; `nbuf` distinct weight buffers rotate so W streams from HBM (8 x 58.7
     MB > the 256 MB Infinity Cache; a column shard rotates enough copies to exceed it too).
     GB/s counts K*N int8 codes + N scales + M*K x + M*N y per call.  `cols` keeps the first
-    columns (one GPU's column shard); `wdeq` is the oracle's dequantized W when already made."""
+    columns (one GPU's column shard); `wdeq` is the oracle's dequantized W when already made.
+    `packed`: each buffer rearranged once, before the timed region, into the decode-packed
+    layout (the same bytes for N a multiple of 128) and multiplied by gemv_int8w_packed."""
     x16, codes, scales = W.decode()
     if cols is not None:
         codes, scales = np.ascontiguousarray(codes[:, :cols]), np.ascontiguousarray(scales[:cols])
@@ -173,7 +175,12 @@ def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=N
     tx, ts = _t(torch, x), _t(torch, scales)
     out = torch.empty((m, codes.shape[1]), dtype=torch.float32, device="cuda:0")
     tcodes = [_t(torch, codes)] + [_t(torch, np.roll(codes, i, axis=1)) for i in range(1, nbuf)]
-    plans = [D.Plan(tx, tc, scales=ts, out=out) for tc in tcodes]
+    if packed:
+        pw = [D.pack_int8w(tc) for tc in tcodes]
+        del tcodes
+        plans = [D.PackedPlan(tx, p, ts, out=out) for p in pw]
+    else:
+        plans = [D.Plan(tx, tc, scales=ts, out=out) for tc in tcodes]
     res = _timed(plans, max(steps, 2 * nbuf), warmup, torch, runs)
     ms = res["ms"]
     k, n = codes.shape
@@ -665,6 +672,10 @@ def main():
         for m in (1, 4, 16):
             extra[f"decode_m{m}"] = bench_decode(torch, D, W, O, m, args.steps, args.warmup, check, runs=R,
                                                  wdeq=wdeq)
+        # the same products on weights rearranged once into the decode-packed layout
+        for m in (1, 4, 16):
+            extra[f"decode_m{m}_packed"] = bench_decode(torch, D, W, O, m, args.steps, args.warmup, check, runs=R,
+                                                        wdeq=wdeq, packed=True)
         x, wb = W.swiglu_up()
         extra["swiglu_up"] = bench_product(
             torch, D, x, wb, max(3, args.steps // 4), max(3, args.warmup // 10),
@@ -677,6 +688,8 @@ def main():
         # one GPU's share of the two products a column split spreads over 8 GPUs: N/8 columns
         extra["shard_decode_m1_n1792"] = bench_decode(torch, D, W, O, 1, args.steps, args.warmup, check,
                                                       runs=R, cols=14336 // 8, wdeq=wdeq)
+        extra["shard_decode_m1_n1792_packed"] = bench_decode(torch, D, W, O, 1, args.steps, args.warmup, check,
+                                                             runs=R, cols=14336 // 8, wdeq=wdeq, packed=True)
         extra["shard_prefill_n512"] = bench_prefill(torch, D, W, O, args.steps, args.warmup, check, runs=R,
                                                     cols=4096 // 8)
         extra["shard_prefill_n512"].pop("out")

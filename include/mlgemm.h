@@ -119,6 +119,35 @@ int mlg_gemm_ws(float* c, const void* a, const void* b, const float* scales, con
 int mlg_gemm_noalloc(float* c, const void* a, const void* b, const float* scales, const float* bias, int64_t m,
                      int64_t n, int64_t k, int32_t op, int32_t a_type, int32_t b_type, int64_t leaf, void* stream);
 
+/* Decode-packed int8 weights.  No counterpart in the reference: its int8 weights are row-major
+ * codes converted to float32 before any product (python/mojolearn/lowbit.py:1-20); this is a
+ * layout of this build's int8-weight decode path (mlg_gemm_int8w / mlg_gemm_ws with b_type 2,
+ * op NN), for callers that keep a weight resident across many decode steps and can rearrange
+ * it once.  codes[k][n] (k a positive multiple of 128 with at most 1024 leaves of 128, n >= 1)
+ * becomes a copy of mlg_int8w_packed_bytes(k, n) = k * 128 * ceil(n / 128) bytes in which code
+ * (p, j) sits at ((o * P + t) * G + g) * 1024 + l * 16 + i * 2 + e, with P = k / 128 leaves,
+ * t = p / 128, o = (p % 128) / 8, i = p % 8, G = ceil(n / 128) groups, g = j / 128,
+ * l = (j % 128) / 2, e = j % 2 (columns past n are zero codes): the eight rows of one lane's two
+ * columns are one 16-byte word, and every leaf's octet o is one contiguous slab, so the decode
+ * kernel's waves, which advance together, read one slab at a time.
+ * mlg_int8w_pack writes the copy (dst 16-byte aligned) on `stream`; -1 / an error for a shape
+ * the layout does not take. */
+int64_t mlg_int8w_packed_bytes(int64_t k, int64_t n);
+int mlg_int8w_pack(void* dst, const int8_t* codes, int64_t k, int64_t n, void* stream);
+
+/* C[m][n] = X[m][k] . W_deq (+ bias) from a decode-packed W, 1 <= m <= 16: the same bits as
+ * mlg_gemm_ws(c, x, codes, scales, bias, m, n, k, op 0, a_type 0, b_type 2, leaf 0, ...) on the
+ * row-major codes (the contract's 128-step leaves, chains, tree, bias and store).  `workspace`
+ * holds mlg_gemv_int8w_packed_workspace_bytes(m, n, k) bytes (0 when the leaves fit one
+ * workgroup; NULL then accepted); its first mlg_gemv_int8w_packed_counter_bytes(m, n, k) bytes
+ * are completion counters, zeroed before its first product and left zero by every product (as
+ * for mlg_gemm_ws).  Calls sharing a workspace must be ordered.  -1 from the size queries for a
+ * shape the entry does not take. */
+int64_t mlg_gemv_int8w_packed_workspace_bytes(int64_t m, int64_t n, int64_t k);
+int64_t mlg_gemv_int8w_packed_counter_bytes(int64_t m, int64_t n, int64_t k);
+int mlg_gemv_int8w_packed(float* c, const float* x, const void* packed, const float* scales, const float* bias,
+                          int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Bytes of workspace mlg_gemm_ws needs for this product on the current device, for operands
  * a, b at these addresses (an operand the tile kernel cannot load in place -- base not 16-byte
  * aligned, rows not a multiple of 16 bytes -- is repacked into the workspace); -1 on error.

@@ -99,6 +99,16 @@ def lib():
         L.mlg_gemm_int15i64_ws.restype = ctypes.c_int
         L.mlg_stream_read.argtypes = [vp, i64, i64, i32, vp, vp]
         L.mlg_stream_read.restype = ctypes.c_int
+        L.mlg_int8w_packed_bytes.argtypes = [i64, i64]
+        L.mlg_int8w_packed_bytes.restype = i64
+        L.mlg_int8w_pack.argtypes = [vp, vp, i64, i64, vp]
+        L.mlg_int8w_pack.restype = ctypes.c_int
+        L.mlg_gemv_int8w_packed_workspace_bytes.argtypes = [i64, i64, i64]
+        L.mlg_gemv_int8w_packed_workspace_bytes.restype = i64
+        L.mlg_gemv_int8w_packed_counter_bytes.argtypes = [i64, i64, i64]
+        L.mlg_gemv_int8w_packed_counter_bytes.restype = i64
+        L.mlg_gemv_int8w_packed.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, vp, i64, vp]
+        L.mlg_gemv_int8w_packed.restype = ctypes.c_int
         L.mlg_last_error.argtypes = []
         L.mlg_last_error.restype = ctypes.c_char_p
         for name in ("mlg_numeric_mode", "mlg_profile_version", "mlg_lowbit_profile_version"):

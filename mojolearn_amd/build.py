@@ -24,7 +24,7 @@ FLAGS = [
     # packed fp32 (v_pk_fma_f32 and friends) stays off in every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["gemv_nn.hip", "gemv_nt.hip", "gemv_mfma.hip", "gemm_mfma.hip", "gemm_q8.hip", "kernels.hip", "follow.hip", "transport.hip", "stream_read.hip", "capi.hip"]
+SOURCES = ["gemv_nn.hip", "gemv_nt.hip", "gemv_mfma.hip", "gemv_packed.hip", "gemm_mfma.hip", "gemm_q8.hip", "kernels.hip", "follow.hip", "transport.hip", "stream_read.hip", "capi.hip"]
 
 
 def _clean(stderr):

@@ -728,6 +728,45 @@ int64_t mlg_gemm_route(const void* a, const void* b, int64_t m, int64_t n, int64
 
 // The memory floors of the skinny products, for bench.py (not part of the reference's
 // interface, so not in include/mlgemm.h).
+int64_t mlg_int8w_packed_bytes(int64_t k, int64_t n) { return mlg::int8w_packed_bytes(k, n); }
+
+int mlg_int8w_pack(void* dst, const int8_t* codes, int64_t k, int64_t n, void* stream) {
+  return guarded([&] {
+    if (mlg::int8w_packed_bytes(k, n) < 0)
+      throw Fail("mlg_int8w_pack: k must be a positive multiple of 128 with at most 1024 leaves, n >= 1; got k=" +
+                 std::to_string(k) + ", n=" + std::to_string(n));
+    if (!dst || !codes) throw Fail("mlg_int8w_pack: null buffer");
+    if ((uintptr_t)dst % 16 != 0) throw Fail("mlg_int8w_pack: the packed buffer must be 16-byte aligned");
+    hip_check(mlg::run_int8w_pack(dst, codes, k, n, static_cast<hipStream_t>(stream)), "int8w pack launch");
+  });
+}
+
+int64_t mlg_gemv_int8w_packed_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (!mlg::gemv_packed_limit(m, n, k, nullptr).empty()) return -1;
+  return mlg::gemv_packed_workspace_floats(m, n, k) * (int64_t)sizeof(float);
+}
+
+int64_t mlg_gemv_int8w_packed_counter_bytes(int64_t m, int64_t n, int64_t k) {
+  if (!mlg::gemv_packed_limit(m, n, k, nullptr).empty()) return -1;
+  return mlg::gemv_packed_counter_count(m, n, k) * (int64_t)sizeof(unsigned int);
+}
+
+int mlg_gemv_int8w_packed(float* c, const float* x, const void* packed, const float* scales, const float* bias,
+                          int64_t m, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes, void* stream) {
+  return guarded([&] {
+    const std::string why = mlg::gemv_packed_limit(m, n, k, packed);
+    if (!why.empty()) throw Fail("mlg_gemv_int8w_packed: " + why + "; got " + shape_text(m, n, k));
+    if (!c || !x || !packed || !scales) throw Fail("mlg_gemv_int8w_packed: null buffer");
+    const int64_t need = mlg::gemv_packed_workspace_floats(m, n, k) * (int64_t)sizeof(float);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+      throw Fail("mlg_gemv_int8w_packed: workspace of " + std::to_string(workspace_bytes) + " bytes is smaller than the " +
+                 std::to_string(need) + " this product needs");
+    hip_check(mlg::run_gemv_packed(c, x, packed, scales, bias, m, n, k, static_cast<float*>(workspace),
+                                   num_cus_of_current_device(), static_cast<hipStream_t>(stream)),
+              "packed gemv launch");
+  });
+}
+
 int mlg_stream_read(const void* w, int64_t rows, int64_t cols, int32_t pattern, uint32_t* sink, void* stream) {
   return guarded([&] {
     hip_check(mlg::run_stream_read(w, rows, cols, pattern, sink, static_cast<hipStream_t>(stream)),

@@ -68,6 +68,23 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
 
 // Zero `count` words on `stream` with a kernel.
 hipError_t run_zero_words(unsigned int* p, int64_t count, hipStream_t stream);
+
+// int8 weights W[k][n] in the decode-packed layout (gemv_packed.hip): k a multiple of 128 with at
+// most 1024 leaves, n >= 1.  Bytes of the packed copy (k * 128 * ceil(n / 128)), or -1 for a
+// shape the layout does not take.
+int64_t int8w_packed_bytes(int64_t k, int64_t n);
+// Write the packed copy of codes[k][n] to dst (16-byte aligned, int8w_packed_bytes bytes).
+hipError_t run_int8w_pack(void* dst, const int8_t* codes, int64_t k, int64_t n, hipStream_t stream);
+// Workspace floats run_gemv_packed needs: [completion counters][group roots], 0 for one group.
+int64_t gemv_packed_workspace_floats(int64_t m, int64_t n, int64_t k);
+// Words of completion counters at the start of that workspace (zero before its first product;
+// every product leaves them zero).
+int64_t gemv_packed_counter_count(int64_t m, int64_t n, int64_t k);
+// C[m][n] = X[m][k] . W_deq (+ bias) from the packed copy, 1 <= m <= 16: the bits of run_gemm on
+// the row-major codes (OP_NN, int8, the contract's leaves).  Empty string, or why it was refused.
+std::string gemv_packed_limit(int64_t m, int64_t n, int64_t k, const void* packed);
+hipError_t run_gemv_packed(float* c, const float* x, const void* packed, const float* scales, const float* bias,
+                           int64_t m, int64_t n, int64_t k, float* ws, int num_cus, hipStream_t stream);
 // Read-only streams over an int8 matrix W[rows][cols] (stream_read.hip): pattern 0 the whole
 // matrix in address order, pattern 1 the decode kernel's leaf-by-leaf reads.  Measurement only.
 hipError_t run_stream_read(const void* w, int64_t rows, int64_t cols, int pattern, uint32_t* sink,

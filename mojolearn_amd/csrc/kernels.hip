@@ -319,6 +319,58 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
   return launch_fold_groups(p.c, ldc, ws, p.m, p.n, g.ngroups, epi, epi_p, p.act, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Decode-packed int8 weights (gemv_packed.hip)
+
+static constexpr int64_t PK_GROUP_COLS = 128;
+
+int64_t int8w_packed_bytes(int64_t k, int64_t n) {
+  if (k <= 0 || n <= 0 || k % GV_CH != 0 || k / GV_CH > MAX_LEAVES) return -1;
+  return k * PK_GROUP_COLS * ((n + PK_GROUP_COLS - 1) / PK_GROUP_COLS);
+}
+
+hipError_t run_int8w_pack(void* dst, const int8_t* codes, int64_t k, int64_t n, hipStream_t stream) {
+  if (int8w_packed_bytes(k, n) < 0 || !dst || !codes || !aligned(dst, 16)) return hipErrorInvalidValue;
+  return launch_int8w_pack(dst, codes, k, n, stream);
+}
+
+int64_t gemv_packed_counter_count(int64_t m, int64_t n, int64_t k) {
+  if (int8w_packed_bytes(k, n) < 0 || m < 1 || m > GV_MAXM || gemv_groups(k / GV_CH) <= 1) return 0;
+  return (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS;
+}
+
+int64_t gemv_packed_workspace_floats(int64_t m, int64_t n, int64_t k) {
+  const int64_t cnt = gemv_packed_counter_count(m, n, k);
+  // sized for 4-leaf groups, the most groups either workgroup width makes
+  return cnt > 0 ? round_floats(cnt) + gemv_groups(k / GV_CH) * m * n : 0;
+}
+
+std::string gemv_packed_limit(int64_t m, int64_t n, int64_t k, const void* packed) {
+  if (m < 1 || m > GV_MAXM) return "m must be 1 .. 16";
+  if (int8w_packed_bytes(k, n) < 0) return "k must be a positive multiple of 128 with at most 1024 leaves, n >= 1";
+  if (packed && !aligned(packed, 16)) return "the packed weights must be 16-byte aligned";
+  const int64_t ncg = (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS;
+  if (ncg * gemv_groups(k / GV_CH) > INT32_MAX) return "more workgroups than one launch holds";
+  return "";
+}
+
+hipError_t run_gemv_packed(float* c, const float* x, const void* packed, const float* scales, const float* bias,
+                           int64_t m, int64_t n, int64_t k, float* ws, int num_cus, hipStream_t stream) {
+  if (!gemv_packed_limit(m, n, k, packed).empty() || !c || !x || !packed || !scales) return hipErrorInvalidValue;
+  const int64_t P = k / GV_CH, ncg = (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS;
+  GemvArgs v;
+  v.c = c; v.w = packed; v.scales = scales; v.bias = bias;
+  v.m = m; v.n = n; v.k = k; v.leaf = GV_CH; v.nleaves = P; v.ncg = ncg;
+  // eight leaves a workgroup for the decode rows when the launch still has a workgroup per CU
+  const int64_t wide = (P + GV_WIDE_LEAVES - 1) / GV_WIDE_LEAVES;
+  const int leaves = m <= 2 && ncg * wide >= num_cus ? GV_WIDE_LEAVES : GV_LEAVES;
+  v.ngroups = (P + leaves - 1) / leaves;
+  v.counter = reinterpret_cast<unsigned int*>(ws);
+  v.ws = ws ? ws + round_floats(gemv_packed_counter_count(m, n, k)) : nullptr;
+  if (v.ngroups > 1 && ws == nullptr) return hipErrorInvalidValue;
+  return launch_gemv_packed(v, x, leaves, dim3((unsigned)(ncg * v.ngroups)), stream);
+}
+
 // Zero `count` 32-bit words (the completion counters of a skinny product) with a kernel: a
 // memset node would not be safe in a captured graph.
 __global__ void zero_words_kernel(unsigned int* p, int64_t count) {

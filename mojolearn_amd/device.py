@@ -287,6 +287,85 @@ class Plan:
         return self.out
 
 
+# ---- decode-packed int8 weights (mlg_int8w_pack / mlg_gemv_int8w_packed)
+
+class PackedInt8W:
+    """int8 codes[k][n] rearranged once for the decode GEMV: `data` is a 1-D uint8 device tensor
+    of mlg_int8w_packed_bytes(k, n) bytes; `k` and `n` are the codes' shape."""
+
+    def __init__(self, data, k, n):
+        self.data, self.k, self.n = data, int(k), int(n)
+
+    def __repr__(self):
+        return f"PackedInt8W(k={self.k}, n={self.n}, bytes={self.data.numel()})"
+
+
+def pack_int8w(codes):
+    """The decode-packed copy of int8 codes[k][n] (k a positive multiple of 128, at most 1024
+    leaves of 128), written on the current stream."""
+    _check(codes, "codes", torch.int8)
+    if codes.dim() != 2:
+        raise ValueError("codes must be 2-D [k, n]")
+    k, n = codes.shape
+    nb = _native.lib().mlg_int8w_packed_bytes(k, n)
+    if nb < 0:
+        raise ValueError(f"the decode-packed layout takes k a positive multiple of 128 (at most 1024 leaves), got k={k}")
+    data = torch.empty(nb, dtype=torch.uint8, device=codes.device)
+    with torch.cuda.device(codes.device):
+        _native.check(_native.lib().mlg_int8w_pack(data.data_ptr(), codes.data_ptr(), k, n, _stream(codes)))
+    return PackedInt8W(data, k, n)
+
+
+def _packed_args(x, packed, scales):
+    _check(x, "x", torch.float32)
+    if not isinstance(packed, PackedInt8W):
+        raise TypeError("packed must be a PackedInt8W (from pack_int8w)")
+    _check(scales, "scales", torch.float32)
+    if x.dim() != 2 or x.shape[1] != packed.k:
+        raise ValueError(f"x must be [m, {packed.k}], got {tuple(x.shape)}")
+    if scales.numel() != packed.n:
+        raise ValueError(f"scales must hold n={packed.n} values")
+    m = x.shape[0]
+    nb = _native.lib().mlg_gemv_int8w_packed_workspace_bytes(m, packed.n, packed.k)
+    if nb < 0:
+        raise ValueError(f"the packed decode product takes 1 <= m <= 16, got m={m}")
+    return m, nb
+
+
+def gemv_int8w_packed(x, packed, scales, *, bias=None, out=None):
+    """C = x . W_deq (+ bias) from decode-packed weights, 1 <= m <= 16: the bits of
+    gemm_int8w(x, codes, scales, bias=bias) on the row-major codes."""
+    m, nb = _packed_args(x, packed, scales)
+    c = _prep_out(out, m, packed.n, x)
+    ws = torch.zeros(max(nb, 4), dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        _native.check(_native.lib().mlg_gemv_int8w_packed(c.data_ptr(), x.data_ptr(), packed.data.data_ptr(),
+                                                          scales.data_ptr(), _bias(bias, packed.n), m, packed.n,
+                                                          packed.k, ws.data_ptr(), nb, _stream(x)))
+    return c
+
+
+class PackedPlan:
+    """gemv_int8w_packed's arguments bound once (workspace allocated and zeroed), so that a call
+    is a single C entry with no allocation and no synchronization -- capturable in a HIP graph."""
+
+    def __init__(self, x, packed, scales, *, bias=None, out=None):
+        m, nb = _packed_args(x, packed, scales)
+        self.out = _prep_out(out, m, packed.n, x)
+        self.ws = torch.zeros(max(nb, 4), dtype=torch.uint8, device=x.device)
+        self.args = (self.out.data_ptr(), x.data_ptr(), packed.data.data_ptr(), scales.data_ptr(),
+                     _bias(bias, packed.n), m, packed.n, packed.k, self.ws.data_ptr(), nb)
+        self._keep = (x, packed, scales, bias)
+        self._fn = _native.lib().mlg_gemv_int8w_packed
+
+    def __call__(self, stream=None):
+        s = stream.cuda_stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        rc = self._fn(*self.args, s)
+        if rc:
+            _native.check(rc)
+        return self.out
+
+
 # ---- caller-partition and sequence-executor words on strided views
 
 EPI_NONE, EPI_PLUS_BIAS, EPI_BIAS_ACT, EPI_ACT_BWD = 0, 3, 4, 5

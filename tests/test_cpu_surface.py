@@ -41,6 +41,41 @@ def test_stream_read_refuses_before_any_launch():
     assert L.mlg_stream_read(ctypes.addressof(buf), 512, 256, 7, ctypes.addressof(sink), None) == 1
 
 
+def test_int8w_packed_sizes_and_refusals():
+    """The decode-packed int8 entries size their buffers on the host (k * 128 * ceil(n / 128)
+    packed bytes; the row-major decode product's workspace: counters for the 128-column groups,
+    then 4-leaf group roots) and refuse, with a message and before any launch, shapes the layout
+    does not take, m past 16, missing buffers, a misaligned packed buffer and a short workspace."""
+    L = _native.lib()
+    assert L.mlg_int8w_packed_bytes(4096, 14336) == 4096 * 14336
+    assert L.mlg_int8w_packed_bytes(4096, 300) == 4096 * 384
+    assert L.mlg_int8w_packed_bytes(128, 1) == 128 * 128
+    for k, n in ((100, 64), (0, 64), (128, 0), (128 * 1025, 4)):
+        assert L.mlg_int8w_packed_bytes(k, n) == -1
+    assert L.mlg_gemv_int8w_packed_workspace_bytes(1, 14336, 4096) == (128 + 8 * 14336) * 4
+    assert L.mlg_gemv_int8w_packed_counter_bytes(1, 14336, 4096) == 112 * 4
+    assert L.mlg_gemv_int8w_packed_workspace_bytes(16, 300, 512) == 0  # 4 leaves: one workgroup
+    assert L.mlg_gemv_int8w_packed_workspace_bytes(17, 300, 512) == -1
+    assert L.mlg_gemv_int8w_packed_workspace_bytes(1, 300, 500) == -1
+    buf = (ctypes.c_uint8 * 64)()
+    base = (ctypes.addressof(buf) + 15) // 16 * 16
+    assert L.mlg_int8w_pack(base, base, 100, 64, None) == 1
+    assert b"mlg_int8w_pack" in L.mlg_last_error()
+    assert L.mlg_int8w_pack(None, base, 128, 64, None) == 1
+    assert L.mlg_int8w_pack(base + 1, base, 128, 64, None) == 1
+    assert b"16-byte" in L.mlg_last_error()
+    ok = (base, base, base, base, None, 1, 64, 512)
+    assert L.mlg_gemv_int8w_packed(base, base, base, base, None, 17, 64, 512, None, 0, None) == 1
+    assert b"m must be" in L.mlg_last_error()
+    assert L.mlg_gemv_int8w_packed(base, base, base, base, None, 1, 64, 500, None, 0, None) == 1
+    assert L.mlg_gemv_int8w_packed(None, *ok[1:], None, 0, None) == 1
+    assert L.mlg_gemv_int8w_packed(base, base, base + 4, base, None, 1, 64, 512, None, 0, None) == 1
+    assert b"16-byte" in L.mlg_last_error()
+    # 4096 rows are 32 leaves: more than one group, so a workspace is required
+    assert L.mlg_gemv_int8w_packed(base, base, base, base, None, 1, 64, 4096, base, 16, None) == 1
+    assert b"workspace" in L.mlg_last_error()
+
+
 def test_metadata_ops():
     assert _native.call(11, [], []) == 1
     assert _native.call(12, [], []) == 1

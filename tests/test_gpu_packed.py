@@ -1,0 +1,131 @@
+"""Decode-packed int8 weights (mlg_int8w_pack, mlg_gemv_int8w_packed), on the GPU.
+
+* The pack kernel's bytes equal a NumPy restatement of the layout (a reshape of the codes to
+  [leaf][octet][row][group][lane][code] and a transpose to [octet][leaf][group][lane][row][code],
+  columns padded with zero codes), which shares no index arithmetic with the kernel.
+* The packed decode product is bit-equal, on poisoned outputs, to the oracle and to the
+  row-major product (gemm_int8w) for 1 <= m <= 16: one workgroup, several, eight-leaf groups
+  with a ragged last group, ragged column groups, special x values, extreme and subnormal
+  scales, with and without the fused bias; again on a second call (counters left zero).
+* A PackedPlan captured in a HIP graph on a fresh stream replays correctly with eager work in
+  between.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+POISON = -987654.0
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _bits(x):
+    return np.ascontiguousarray(x).view(np.uint32)
+
+
+def packed_layout(codes):
+    """The decode-packed bytes of codes[k][n] (k a multiple of 128)."""
+    k, n = codes.shape
+    P, G = k // 128, -(-n // 128)
+    pad = np.zeros((k, G * 128), np.int8)
+    pad[:, :n] = codes
+    a = pad.reshape(P, 16, 8, G, 64, 2).transpose(1, 0, 3, 4, 2, 5)
+    return np.ascontiguousarray(a).reshape(-1).view(np.uint8)
+
+
+@pytest.mark.parametrize("k,n", [(128, 1), (256, 130), (1152, 257), (4096, 300), (4480, 8196)])
+def test_pack_layout(k, n):
+    from mojolearn_amd import device as D
+    rng = np.random.default_rng(k + n)
+    codes = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    packed = D.pack_int8w(_t(codes))
+    torch.cuda.synchronize()
+    got = packed.data.cpu().numpy()
+    assert got.size == k * 128 * (-(-n // 128))
+    assert np.array_equal(got, packed_layout(codes))
+
+
+def _x(rng, m, k, special):
+    x = (rng.standard_normal((m, k)) * np.exp2(rng.uniform(-20, 20, (m, k)))).astype(np.float32)
+    if special:
+        flat = x.reshape(-1)
+        idx = rng.choice(flat.size, min(flat.size, 64), replace=False)
+        vals = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-42, 3e38], np.float32)
+        flat[idx] = vals[np.arange(idx.size) % vals.size]
+    return x
+
+
+PACKED_SHAPES = [(1, 14336, 4096), (2, 300, 640), (1, 1, 128), (1, 130, 256), (3, 257, 1024), (4, 1000, 4096),
+                 (8, 64, 1152), (16, 129, 1152), (16, 2048, 4096), (1, 8196, 4480), (2, 4096, 8192), (5, 14336, 4096)]
+
+
+@pytest.mark.parametrize("shape", PACKED_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in PACKED_SHAPES])
+def test_packed_gemv_parity(oracle, shape):
+    from mojolearn_amd import device as D
+    m, n, k = shape
+    rng = np.random.default_rng(m * 31 + n + k)
+    special = (m + n) % 2 == 1
+    x = _x(rng, m, k, special)
+    codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    if special:  # extreme scales: subnormal (flushed on input), zero, huge, tiny normal
+        scales[: min(n, 4)] = np.array([1e-40, 0.0, 3e37, 1.2e-38], np.float32)[: min(n, 4)]
+    bias = rng.standard_normal(n).astype(np.float32) if k % 256 == 0 else None
+    print(f"packed gemv m={m} n={n} k={k} special={special} bias={bias is not None}", flush=True)
+    tx, tc, ts = _t(x), _t(codes), _t(scales)
+    tb = None if bias is None else _t(bias)
+    packed = D.pack_int8w(tc)
+    want = oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0)
+    if bias is not None:
+        want = oracle.bias(want, bias)
+    want = oracle.nan_canon(want)
+    for call in range(2):  # a second call: the completion counters were left zero
+        out = torch.full((m, n), POISON, dtype=torch.float32, device=DEV)
+        D.gemv_int8w_packed(tx, packed, ts, bias=tb, out=out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        bad = np.flatnonzero(_bits(got) != _bits(want))
+        assert bad.size == 0, f"call {call}: {bad.size} words differ, first at {divmod(int(bad[0]), n)}"
+    rowmajor = D.gemm_int8w(tx, tc, ts, bias=tb).cpu().numpy()
+    assert np.array_equal(_bits(rowmajor), _bits(got))
+
+
+def test_packed_plan_captured_on_a_fresh_stream(oracle):
+    from mojolearn_amd import device as D
+    rng = np.random.default_rng(303)
+    m, n, k = 1, 14336, 4096
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    want = oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0)
+    packed = D.pack_int8w(_t(codes))
+    plan = D.PackedPlan(_t(x), packed, _t(scales))
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        plan(s)
+    for rep in range(3):
+        plan.out.fill_(POISON)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(plan.out.cpu().numpy()), _bits(want)), f"replay {rep}"
+        D.gemm(_t(x), _t(np.ascontiguousarray(codes[:, :300], dtype=np.float32)))  # eager work between
+
+
+def test_packed_refusals():
+    from mojolearn_amd import device as D
+    codes = torch.zeros((100, 64), dtype=torch.int8, device=DEV)
+    with pytest.raises(ValueError, match="multiple of 128"):
+        D.pack_int8w(codes)
+    packed = D.pack_int8w(torch.zeros((128, 64), dtype=torch.int8, device=DEV))
+    scales = torch.ones(64, dtype=torch.float32, device=DEV)
+    with pytest.raises(ValueError, match="1 <= m <= 16"):
+        D.gemv_int8w_packed(torch.zeros((17, 128), dtype=torch.float32, device=DEV), packed, scales)
+    with pytest.raises(ValueError, match=r"x must be \[m, 128\]"):
+        D.gemv_int8w_packed(torch.zeros((1, 256), dtype=torch.float32, device=DEV), packed, scales)
