@@ -124,12 +124,11 @@ int mlg_gemm_noalloc(float* c, const void* a, const void* b, const float* scales
  * layout of this build's int8-weight decode path (mlg_gemm_int8w / mlg_gemm_ws with b_type 2,
  * op NN), for callers that keep a weight resident across many decode steps and can rearrange
  * it once.  codes[k][n] (k a positive multiple of 128 with at most 1024 leaves of 128, n >= 1)
- * becomes a copy of mlg_int8w_packed_bytes(k, n) = k * 128 * ceil(n / 128) bytes in which code
- * (p, j) sits at ((o * P + t) * G + g) * 1024 + l * 16 + i * 2 + e, with P = k / 128 leaves,
- * t = p / 128, o = (p % 128) / 8, i = p % 8, G = ceil(n / 128) groups, g = j / 128,
- * l = (j % 128) / 2, e = j % 2 (columns past n are zero codes): the eight rows of one lane's two
- * columns are one 16-byte word, and every leaf's octet o is one contiguous slab, so the decode
- * kernel's waves, which advance together, read one slab at a time.
+ * becomes a copy of mlg_int8w_packed_bytes(k, n) = k * 64 * ceil(n / 64) bytes in which code
+ * (p, j) sits at ((s * P + t) * G + g) * 1024 + l * 16 + i, with P = k / 128 leaves,
+ * t = p / 128, s = (p % 128) / 16, i = p % 16, G = ceil(n / 64) groups, g = j / 64, l = j % 64
+ * (columns past n are zero codes): sixteen rows of one column are one 16-byte word, a 64-column
+ * group's block is one 1 KB chunk, and block s of every leaf is one contiguous slab.
  * mlg_int8w_pack writes the copy (dst 16-byte aligned) on `stream`; -1 / an error for a shape
  * the layout does not take. */
 int64_t mlg_int8w_packed_bytes(int64_t k, int64_t n);
@@ -138,8 +137,8 @@ int mlg_int8w_pack(void* dst, const int8_t* codes, int64_t k, int64_t n, void* s
 /* C[m][n] = X[m][k] . W_deq (+ bias) from a decode-packed W, 1 <= m <= 16: the same bits as
  * mlg_gemm_ws(c, x, codes, scales, bias, m, n, k, op 0, a_type 0, b_type 2, leaf 0, ...) on the
  * row-major codes (the contract's 128-step leaves, chains, tree, bias and store).  `workspace`
- * holds mlg_gemv_int8w_packed_workspace_bytes(m, n, k) bytes (0 when the leaves fit one
- * workgroup; NULL then accepted); its first mlg_gemv_int8w_packed_counter_bytes(m, n, k) bytes
+ * holds mlg_gemv_int8w_packed_workspace_bytes(m, n, k) bytes (0 when k <= 512; NULL then
+ * accepted; at K = 4096 on a GPU that the launch fills, no byte of it is used); its first mlg_gemv_int8w_packed_counter_bytes(m, n, k) bytes
  * are completion counters, zeroed before its first product and left zero by every product (as
  * for mlg_gemm_ws).  Calls sharing a workspace must be ordered.  -1 from the size queries for a
  * shape the entry does not take. */

@@ -81,9 +81,13 @@ hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, di
 // 2 <= m <= 8 on the 4 x 4 shape (same conditions as the 16 x 16 kernel).
 hipError_t launch_gemv_mfma4_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, dim3 grid,
                                 hipStream_t stream);
-// The decode-packed int8 layout (gemv_packed.hip): `leaves` per workgroup GV_LEAVES, or
-// GV_WIDE_LEAVES for m <= 2.
-hipError_t launch_gemv_packed(const GemvArgs& g, const float* x, int leaves, dim3 grid, hipStream_t stream);
+// The decode-packed int8 layout (gemv_packed.hip): 64-column groups, two leaves a wave, `waves`
+// a workgroup: PK_WAVES_WHOLE (32 leaves, the whole tree at K = 4096) when the launch fills the
+// CUs, else PK_WAVES_SPLIT (4 leaves, group roots folded across workgroups).
+constexpr int PK_GROUP_COLS = 64;
+constexpr int PK_WAVES_WHOLE = 16;
+constexpr int PK_WAVES_SPLIT = 2;
+hipError_t launch_gemv_packed(const GemvArgs& g, const float* x, int waves, dim3 grid, hipStream_t stream);
 hipError_t launch_int8w_pack(void* dst, const void* codes, int64_t k, int64_t n, hipStream_t stream);
 // vec (OP_NT): 0 element loads, 1 16-byte loads.
 hipError_t launch_gemv_nt(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,

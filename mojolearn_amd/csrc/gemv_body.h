@@ -357,27 +357,34 @@ __device__ __forceinline__ void gv_fold_pow2(const GemvArgs& g, int tid, int64_t
 // part[wave][row][col]: the workgroup's root (the tree over its up to LEAVES leaves),
 // then either the store (one group) or the count and, in the workgroup that completes it,
 // the fold of every group's root (the rest of the contract's tree), bias and store.
-template <int MR, int COLS, int LEAVES = GV_LEAVES, int THREADS = GV_THREADS>
-__device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[LEAVES][MR][COLS],
+//
+// PAIRED: each wave ran two adjacent leaves and wrote their level-1 node (the pair's sum, or the
+// odd last leaf carried), so part holds LEAVES / 2 nodes -- the tree over them is the rest of the
+// contract's tree over the workgroup's leaves.
+template <int MR, int COLS, int LEAVES = GV_LEAVES, int THREADS = GV_THREADS, bool PAIRED = false>
+__device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[PAIRED ? LEAVES / 2 : LEAVES][MR][COLS],
                                           unsigned int& last_flag, int tid, int64_t grp, int64_t cg, int m) {
-  static_assert(LEAVES == 4 || LEAVES == 8, "a workgroup folds 4 or 8 leaves");
+  constexpr int NODES = PAIRED ? LEAVES / 2 : LEAVES;
+  static_assert(NODES == 2 || NODES == 4 || NODES == 8 || NODES == 16, "a workgroup folds 2 .. 16 nodes");
+  static_assert(PAIRED || LEAVES == 4 || LEAVES == 8, "unpaired workgroups fold 4 or 8 leaves");
   __syncthreads();
   const int64_t left = g.nleaves - grp * LEAVES;
-  const int cnt = left < LEAVES ? (int)left : LEAVES;
+  const int cntl = left < LEAVES ? (int)left : LEAVES;
+  const int cnt = PAIRED ? (cntl + 1) / 2 : cntl;  // nodes written
   constexpr int CPT = (MR * COLS + THREADS - 1) / THREADS;  // cells per thread
   constexpr int LB = CPT < 4 ? CPT : 4;                      // cells per batch of LDS reads
   // this thread's cells tid + c * THREADS of rows < m, LB at a time: every partial of a
   // batch read before any add
 #pragma unroll
   for (int c0 = 0; c0 < CPT; c0 += LB) {
-    float p[LEAVES][LB];
+    float p[NODES][LB];
 #pragma unroll
     for (int c = 0; c < LB; ++c) {
       const int cell = tid + (c0 + c) * THREADS;
       const int r = cell / COLS, col = cell % COLS;
       if (c0 + c >= CPT || cell >= MR * COLS || r >= m) continue;
 #pragma unroll
-      for (int l = 0; l < LEAVES; ++l)
+      for (int l = 0; l < NODES; ++l)
         if (l < cnt) p[l][c] = part[l][r][col];
     }
 #pragma unroll
@@ -387,29 +394,29 @@ __device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[LEAVE
       const int64_t j = cg * COLS + col;
       if (c0 + c >= CPT || cell >= MR * COLS || r >= m || j >= g.n) continue;
       float y;
-      if (cnt == LEAVES) {
+      if (cnt == NODES) {
         // the complete aligned subtree: adjacent pairs, level by level
-        float v[LEAVES];
+        float v[NODES];
 #pragma unroll
-        for (int l = 0; l < LEAVES; ++l) v[l] = p[l][c];
+        for (int l = 0; l < NODES; ++l) v[l] = p[l][c];
 #pragma unroll
-        for (int w = LEAVES; w > 1; w /= 2)
+        for (int w = NODES; w > 1; w /= 2)
 #pragma unroll
           for (int q = 0; q < w / 2; ++q) v[q] = v[2 * q] + v[2 * q + 1];
         y = v[0];
       } else {
         // the tail of the tree (the last group, fewer leaves): the odd one carried up
-        float v[LEAVES];
+        float v[NODES];
 #pragma unroll
-        for (int l = 0; l < LEAVES; ++l) v[l] = l < cnt ? p[l][c] : 0.f;
+        for (int l = 0; l < NODES; ++l) v[l] = l < cnt ? p[l][c] : 0.f;
         int w = cnt;
 #pragma unroll 1
         while (w > 1) {
 #pragma unroll
-          for (int q = 0; q < LEAVES / 2; ++q)
+          for (int q = 0; q < NODES / 2; ++q)
             if (q < w / 2) v[q] = v[2 * q] + v[2 * q + 1];
 #pragma unroll
-          for (int q = 0; q < LEAVES / 2; ++q)
+          for (int q = 0; q < NODES / 2; ++q)
             if ((w & 1) && q == w / 2) v[q] = v[w - 1];
           w = (w + 1) / 2;
         }

@@ -322,11 +322,22 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
 // ---------------------------------------------------------------------------
 // Decode-packed int8 weights (gemv_packed.hip)
 
-static constexpr int64_t PK_GROUP_COLS = 128;
+static int64_t pk_groups(int64_t n) { return (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS; }
+
+// Waves a workgroup of the packed product: for the decode rows (m <= 2; more rows would spill
+// the x values a 16-wave workgroup keeps in scalar registers) the whole-column workgroups (32
+// leaves) when the launch still holds a workgroup for three of every four CUs, else 4-leaf groups.
+static int pk_waves(int64_t m, int64_t n, int64_t k, int num_cus) {
+  const int64_t P = k / GV_CH, whole = 2 * PK_WAVES_WHOLE;
+  const bool fills = pk_groups(n) * ((P + whole - 1) / whole) * 4 >= 3 * (int64_t)num_cus;
+  return m <= 2 && fills ? PK_WAVES_WHOLE : PK_WAVES_SPLIT;
+}
+
+static int64_t pk_ngroups(int64_t k, int waves) { return (k / GV_CH + 2 * waves - 1) / (2 * waves); }
 
 int64_t int8w_packed_bytes(int64_t k, int64_t n) {
   if (k <= 0 || n <= 0 || k % GV_CH != 0 || k / GV_CH > MAX_LEAVES) return -1;
-  return k * PK_GROUP_COLS * ((n + PK_GROUP_COLS - 1) / PK_GROUP_COLS);
+  return k * PK_GROUP_COLS * pk_groups(n);
 }
 
 hipError_t run_int8w_pack(void* dst, const int8_t* codes, int64_t k, int64_t n, hipStream_t stream) {
@@ -334,41 +345,40 @@ hipError_t run_int8w_pack(void* dst, const int8_t* codes, int64_t k, int64_t n, 
   return launch_int8w_pack(dst, codes, k, n, stream);
 }
 
+// The workspace is sized for the narrowest workgroups (the most group roots), whichever width
+// the device's CU count then picks.
 int64_t gemv_packed_counter_count(int64_t m, int64_t n, int64_t k) {
-  if (int8w_packed_bytes(k, n) < 0 || m < 1 || m > GV_MAXM || gemv_groups(k / GV_CH) <= 1) return 0;
-  return (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS;
+  if (int8w_packed_bytes(k, n) < 0 || m < 1 || m > GV_MAXM || pk_ngroups(k, PK_WAVES_SPLIT) <= 1) return 0;
+  return pk_groups(n);
 }
 
 int64_t gemv_packed_workspace_floats(int64_t m, int64_t n, int64_t k) {
   const int64_t cnt = gemv_packed_counter_count(m, n, k);
-  // sized for 4-leaf groups, the most groups either workgroup width makes
-  return cnt > 0 ? round_floats(cnt) + gemv_groups(k / GV_CH) * m * n : 0;
+  return cnt > 0 ? round_floats(cnt) + pk_ngroups(k, PK_WAVES_SPLIT) * m * n : 0;
 }
 
 std::string gemv_packed_limit(int64_t m, int64_t n, int64_t k, const void* packed) {
   if (m < 1 || m > GV_MAXM) return "m must be 1 .. 16";
   if (int8w_packed_bytes(k, n) < 0) return "k must be a positive multiple of 128 with at most 1024 leaves, n >= 1";
   if (packed && !aligned(packed, 16)) return "the packed weights must be 16-byte aligned";
-  const int64_t ncg = (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS;
-  if (ncg * gemv_groups(k / GV_CH) > INT32_MAX) return "more workgroups than one launch holds";
+  // the loads' leaf stride (ncg KB) in a 32-bit offset, and the grid
+  if (pk_groups(n) * 1024 + 1024 > INT32_MAX) return "n too large for the packed product";
+  if (pk_groups(n) * pk_ngroups(k, PK_WAVES_SPLIT) > INT32_MAX) return "more workgroups than one launch holds";
   return "";
 }
 
 hipError_t run_gemv_packed(float* c, const float* x, const void* packed, const float* scales, const float* bias,
                            int64_t m, int64_t n, int64_t k, float* ws, int num_cus, hipStream_t stream) {
   if (!gemv_packed_limit(m, n, k, packed).empty() || !c || !x || !packed || !scales) return hipErrorInvalidValue;
-  const int64_t P = k / GV_CH, ncg = (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS;
+  const int waves = pk_waves(m, n, k, num_cus);
   GemvArgs v;
   v.c = c; v.w = packed; v.scales = scales; v.bias = bias;
-  v.m = m; v.n = n; v.k = k; v.leaf = GV_CH; v.nleaves = P; v.ncg = ncg;
-  // eight leaves a workgroup for the decode rows when the launch still has a workgroup per CU
-  const int64_t wide = (P + GV_WIDE_LEAVES - 1) / GV_WIDE_LEAVES;
-  const int leaves = m <= 2 && ncg * wide >= num_cus ? GV_WIDE_LEAVES : GV_LEAVES;
-  v.ngroups = (P + leaves - 1) / leaves;
+  v.m = m; v.n = n; v.k = k; v.leaf = GV_CH; v.nleaves = k / GV_CH; v.ncg = pk_groups(n);
+  v.ngroups = pk_ngroups(k, waves);
   v.counter = reinterpret_cast<unsigned int*>(ws);
   v.ws = ws ? ws + round_floats(gemv_packed_counter_count(m, n, k)) : nullptr;
   if (v.ngroups > 1 && ws == nullptr) return hipErrorInvalidValue;
-  return launch_gemv_packed(v, x, leaves, dim3((unsigned)(ncg * v.ngroups)), stream);
+  return launch_gemv_packed(v, x, waves, dim3((unsigned)(v.ncg * v.ngroups)), stream);
 }
 
 // Zero `count` 32-bit words (the completion counters of a skinny product) with a kernel: a

@@ -369,5 +369,52 @@ def bias_cases():
     return out
 
 
+def packed_cases(cus=256):
+    """The decode-packed int8 product (family `packed`: int8 codes rearranged once, OP_NN, k a
+    multiple of 128) on the adversarial words: x drawn from the boundary words, scales from the
+    adversarial scale words, in whole-column workgroups (one group, and a second group holding
+    one leaf) and in 4-leaf groups; the window's edge planted through the dequant (code 1 times
+    the scale 2^-63 is the weight 2^-63); the admission A/B's operand kinds; the fused bias on
+    the words."""
+    out = []
+    whole_n = 192 * 64 * 256 // cus  # ceil(n / 64) >= 3/4 of the CUs: whole-column workgroups
+    shapes = [(1, whole_n, 4096), (1, whole_n + 12, 4224), (2, whole_n, 4096), (1, 300, 1024), (2, 300, 384),
+              (16, 300, 1024), (4, 200, 4096)]
+    for s, (m, n, k) in enumerate(shapes):
+        def make(m=m, n=n, k=k, s=s):
+            rng = np.random.default_rng(700 + s)
+            return _draw(m * k, 7, 0, 400 + s).reshape(m, k), rng.integers(-128, 128, (k, n), dtype=np.int8)
+        scales = _scale_words(np.random.default_rng(800 + s), n)
+        out.append(Case(f"draw-packed-m{m}-n{n}-k{k}", "packed", 0, wt="i8", scales=scales, make=make,
+                        shape=(m, n, k)))
+    m, n, k = 1, 300, 256
+    r, p = np.meshgrid(np.arange(m), np.arange(k), indexing="ij")
+    A = np.where((r + p) % 7 == 0, np.array([0x1FFFFFFF], U32).view(F32)[0], F32(0.0)).astype(F32)
+    p2, c = np.meshgrid(np.arange(k), np.arange(n), indexing="ij")
+    codes = np.where((p2 + 2 * c) % 5 == 0, 1, 0).astype(np.int8)
+    out.append(Case("planted-packed-m1", "packed", 0, np.ascontiguousarray(A), codes, wt="i8",
+                    scales=np.full(n, 2.0 ** -63, F32)))
+    m, n, k = 16, 160, 768
+    for kd, kid in enumerate((2, 3, 4, 5)):
+        A = kind_words(m * k, 1000 + 7 * kd, kid).reshape(m, k)
+        codes = np.random.default_rng(1500 + kd).integers(-128, 128, (k, n), dtype=np.int8)
+        scales = np.random.default_rng(1600 + kd).uniform(1e-3, 1e-2, n).astype(F32)
+        name = ("kmixed", "kskew", "kborder", "ksparse")[kd]
+        for mm in (1, 16):
+            out.append(Case(f"{name}-packed-m{mm}", "packed", 0, np.ascontiguousarray(A[:mm]), codes, wt="i8",
+                            scales=scales))
+    w = boundary_words()
+    rng = np.random.default_rng(4343)
+    for m, n, k in ((1, whole_n, 4096), (2, 300, 1024)):
+        A = _draw(m * k, 7, 0, 500 + m + k).reshape(m, k)
+        codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+        codes[:, 1::2] = 0
+        bias = w[rng.integers(0, 64, n)].astype(F32)
+        bias[1:9:2] = np.array([0x80000001, 0x807FFFFF, 0x00000001, 0x80400000], U32).view(F32)
+        out.append(Case(f"bias-packed-m{m}-n{n}", "packed", 0, np.ascontiguousarray(A), codes, wt="i8",
+                        scales=_scale_words(rng, n), bias=bias))
+    return out
+
+
 def all_cases(cus=256):
-    return kat_cases(cus) + boundary_cases(cus) + bias_cases()
+    return kat_cases(cus) + boundary_cases(cus) + bias_cases() + packed_cases(cus)

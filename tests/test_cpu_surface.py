@@ -42,18 +42,18 @@ def test_stream_read_refuses_before_any_launch():
 
 
 def test_int8w_packed_sizes_and_refusals():
-    """The decode-packed int8 entries size their buffers on the host (k * 128 * ceil(n / 128)
-    packed bytes; the row-major decode product's workspace: counters for the 128-column groups,
-    then 4-leaf group roots) and refuse, with a message and before any launch, shapes the layout
+    """The decode-packed int8 entries size their buffers on the host (k * 64 * ceil(n / 64)
+    packed bytes; a workspace of counters for the 64-column groups, then the roots of 4-leaf
+    groups, when there is more than one) and refuse, with a message and before any launch, shapes the layout
     does not take, m past 16, missing buffers, a misaligned packed buffer and a short workspace."""
     L = _native.lib()
     assert L.mlg_int8w_packed_bytes(4096, 14336) == 4096 * 14336
-    assert L.mlg_int8w_packed_bytes(4096, 300) == 4096 * 384
-    assert L.mlg_int8w_packed_bytes(128, 1) == 128 * 128
+    assert L.mlg_int8w_packed_bytes(4096, 300) == 4096 * 320
+    assert L.mlg_int8w_packed_bytes(128, 1) == 128 * 64
     for k, n in ((100, 64), (0, 64), (128, 0), (128 * 1025, 4)):
         assert L.mlg_int8w_packed_bytes(k, n) == -1
-    assert L.mlg_gemv_int8w_packed_workspace_bytes(1, 14336, 4096) == (128 + 8 * 14336) * 4
-    assert L.mlg_gemv_int8w_packed_counter_bytes(1, 14336, 4096) == 112 * 4
+    assert L.mlg_gemv_int8w_packed_workspace_bytes(1, 14336, 4096) == (256 + 8 * 14336) * 4
+    assert L.mlg_gemv_int8w_packed_counter_bytes(1, 14336, 4096) == 224 * 4
     assert L.mlg_gemv_int8w_packed_workspace_bytes(16, 300, 512) == 0  # 4 leaves: one workgroup
     assert L.mlg_gemv_int8w_packed_workspace_bytes(17, 300, 512) == -1
     assert L.mlg_gemv_int8w_packed_workspace_bytes(1, 300, 500) == -1

@@ -1,5 +1,6 @@
 """The closed-form fixtures and the smallest-normal boundary words through every kernel family
-(tests/families.py), on the GPU through the C ABI, against the oracle, bit for bit.
+(tests/families.py), on the GPU through the C ABI, against the oracle, bit for bit -- the
+decode-packed int8 product (family `packed`) through its own entry.
 
 Every output is pre-filled with the reference's poison word -987654.0 (gemm/checks/
 gemm_device_check.mojo:111,535-556), so a cell a kernel leaves unwritten fails; every case first
@@ -33,7 +34,9 @@ def run_gpu(case):
     ta, tb = _t(case.a), _t(case.b.view(np.int16) if case.wt == "bf16" else case.b)
     out = torch.full((case.m, case.n), float(F.POISON), dtype=torch.float32, device=DEV)
     bias = None if case.bias is None else _t(case.bias)
-    if case.wt == "f32":
+    if case.family == "packed":
+        D.gemv_int8w_packed(ta, D.pack_int8w(tb), _t(case.scales), bias=bias, out=out)
+    elif case.wt == "f32":
         D.gemm(ta, tb, op=case.op, bias=bias, out=out, leaf=case.leaf)
     elif case.wt == "bf16":
         D.gemm_bf16w(ta, tb, op=case.op, bias=bias, out=out, leaf=case.leaf)
@@ -51,7 +54,9 @@ def test_family_case(oracle, case):
         ta, tb, got = run_gpu(case)
         cus = torch.cuda.get_device_properties(0).multi_processor_count
         route = D.route(case.m, case.n, case.k, op=case.op, b_type=case.b_type, leaf=case.leaf, a=ta, b=tb)
-        if case.family != "tile_stack" or cus == 256:
+        if case.family == "packed":
+            pass  # its own entry, one kernel
+        elif case.family != "tile_stack" or cus == 256:
             assert _route_name(case) in route, (case.family, route)
         want = case.want(oracle)
         g, w = got.view(np.uint32), want.view(np.uint32)

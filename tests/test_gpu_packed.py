@@ -1,12 +1,14 @@
 """Decode-packed int8 weights (mlg_int8w_pack, mlg_gemv_int8w_packed), on the GPU.
 
 * The pack kernel's bytes equal a NumPy restatement of the layout (a reshape of the codes to
-  [leaf][octet][row][group][lane][code] and a transpose to [octet][leaf][group][lane][row][code],
-  columns padded with zero codes), which shares no index arithmetic with the kernel.
+  [leaf][block][row][group][lane] and a transpose to [block][leaf][group][lane][row], columns
+  padded with zero codes), which shares no index arithmetic with the kernel.
 * The packed decode product is bit-equal, on poisoned outputs, to the oracle and to the
-  row-major product (gemm_int8w) for 1 <= m <= 16: one workgroup, several, eight-leaf groups
-  with a ragged last group, ragged column groups, special x values, extreme and subnormal
-  scales, with and without the fused bias; again on a second call (counters left zero).
+  row-major product (gemm_int8w) for 1 <= m <= 16: whole-column workgroups (32 leaves, one
+  group), whole-column workgroups with a ragged second group and an odd last leaf, 4-leaf
+  groups folded across workgroups, ragged column groups, special x values, extreme and
+  subnormal scales, with and without the fused bias; again on a second call (counters left
+  zero).
 * A PackedPlan captured in a HIP graph on a fresh stream replays correctly with eager work in
   between.
 """
@@ -30,10 +32,10 @@ def _bits(x):
 def packed_layout(codes):
     """The decode-packed bytes of codes[k][n] (k a multiple of 128)."""
     k, n = codes.shape
-    P, G = k // 128, -(-n // 128)
-    pad = np.zeros((k, G * 128), np.int8)
+    P, G = k // 128, -(-n // 64)
+    pad = np.zeros((k, G * 64), np.int8)
     pad[:, :n] = codes
-    a = pad.reshape(P, 16, 8, G, 64, 2).transpose(1, 0, 3, 4, 2, 5)
+    a = pad.reshape(P, 8, 16, G, 64).transpose(1, 0, 3, 4, 2)
     return np.ascontiguousarray(a).reshape(-1).view(np.uint8)
 
 
@@ -45,7 +47,7 @@ def test_pack_layout(k, n):
     packed = D.pack_int8w(_t(codes))
     torch.cuda.synchronize()
     got = packed.data.cpu().numpy()
-    assert got.size == k * 128 * (-(-n // 128))
+    assert got.size == k * 64 * (-(-n // 64))
     assert np.array_equal(got, packed_layout(codes))
 
 
@@ -59,8 +61,12 @@ def _x(rng, m, k, special):
     return x
 
 
+# whole-column workgroups where m <= 2 and ceil(n / 64) * ceil(k / 4096) >= 192 (on 256 CUs):
+# 1x14336x4096 (one group), 1x8196x4480 and 2x12300x4224 (a second group of 3 or 1 leaves: an
+# odd last leaf run alone); the rest in 4-leaf groups
 PACKED_SHAPES = [(1, 14336, 4096), (2, 300, 640), (1, 1, 128), (1, 130, 256), (3, 257, 1024), (4, 1000, 4096),
-                 (8, 64, 1152), (16, 129, 1152), (16, 2048, 4096), (1, 8196, 4480), (2, 4096, 8192), (5, 14336, 4096)]
+                 (8, 64, 1152), (16, 129, 1152), (16, 2048, 4096), (1, 8196, 4480), (2, 4096, 8192), (5, 14336, 4096),
+                 (16, 12288, 4096), (2, 12300, 4224), (1, 1792, 4096), (1, 64, 384)]
 
 
 @pytest.mark.parametrize("shape", PACKED_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in PACKED_SHAPES])
