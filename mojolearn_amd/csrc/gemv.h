@@ -88,6 +88,9 @@ constexpr int PK_GROUP_COLS = 64;
 constexpr int PK_WAVES_WHOLE = 16;
 constexpr int PK_WAVES_SPLIT = 2;
 hipError_t launch_gemv_packed(const GemvArgs& g, const float* x, int waves, dim3 grid, hipStream_t stream);
+// The same product on the matrix cores for 3 <= m <= 16 (x 16-byte aligned, m * k * 4 < 2^31).
+constexpr int PK_MFMA_MIN_M = 3;
+hipError_t launch_gemv_packed_mfma(const GemvArgs& g, const float* x, int waves, dim3 grid, hipStream_t stream);
 hipError_t launch_int8w_pack(void* dst, const void* codes, int64_t k, int64_t n, hipStream_t stream);
 // vec (OP_NT): 0 element loads, 1 16-byte loads.
 hipError_t launch_gemv_nt(const GemvArgs& g, const float* x, int b_type, int64_t m, int vec, dim3 grid,

@@ -184,6 +184,264 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
   gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, true>(g, part, last_flag, tid, grp, cg, m);
 }
 
+// ---- 3 <= m <= 16 on the matrix cores, from the decode-packed layout.
+//
+// Lane l of a wave owns column 64 cg + l (the layout's lane) and feeds B = W[p][64 cg + l] to a
+// K = 1 instruction (one fma_rn per output element: under MODE.FP_DENORM = 2 the contract's
+// fma(ftz a, ftz b, ftz c), like v_fma_f32); A is x[row][p] for the row the shape gives the lane:
+//  * SHAPE 16 (v_mfma_f32_16x16x1_4b_f32, 9 <= m <= 16): block b = l / 16 is the outer product
+//    of lanes 16b .. 16b+15's values, so lane l feeds row l % 16 and gets back, in register
+//    4 blk + i, row 4 (l / 16) + i of column 16 blk + l % 16;
+//  * SHAPE 4 (v_mfma_f32_4x4x1_16b_f32, 3 <= m <= 8, G groups of four rows): lane l feeds row
+//    4 g + l % 4 and gets back, in register r, row 4 g + r of its own column.
+// A wave runs two adjacent leaves, one instruction per leaf per step.  x travels through LDS:
+// each wave streams the x values of its leaves' next blocks (MR rows by 16 steps a leaf) into a
+// ring of its own LDS slots with direct-to-LDS loads, issued with the block's weights, and reads
+// them back four steps at a time.  The workgroup and its fold are gemv_packed_kernel's.
+template <int SHAPE, int G>
+struct PkMf {
+  static constexpr int MR = SHAPE == 16 ? 16 : 4 * G;     // rows the lane's instructions cover
+  static constexpr int NA = SHAPE == 16 ? 1 : G;           // accumulators a leaf
+  static constexpr int CHUNKS = 2 * MR * 4;                // 16-byte x chunks a block: 2 leaves, MR rows, 16 steps
+  static constexpr int NI = CHUNKS < 64 ? 1 : CHUNKS / 64;  // direct-to-LDS loads a block
+  static constexpr int SLOT = NI * 1024;                   // bytes of one ring slot
+};
+typedef float pk_v16f __attribute__((ext_vector_type(16)));
+typedef float pk_v4f __attribute__((ext_vector_type(4)));
+template <int SHAPE>
+using PkV = typename std::conditional<SHAPE == 16, pk_v16f, pk_v4f>::type;
+
+// Chunk c of a slot holds x[r][leaf q, steps 4 u .. 4 u + 3 of the block] with q = c / (4 MR),
+// r = (c / 4) % MR and u = (c % 4) ^ pk_xsw(r): the sixteen rows one read serves land in
+// different LDS banks.
+__device__ __forceinline__ int pk_xsw(int r) { return (r >> 2) & 3; }
+
+// f(integral_constant<int, I>) for I = B .. E-1: the block loop with its index a constant, so
+// every wait count and LDS slot below is named at compile time.
+template <int B, int E, typename F>
+__device__ __forceinline__ void pk_static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    pk_static_for<B + 1, E>(f);
+  }
+}
+
+// s_waitcnt vmcnt(N), other counters untouched
+template <int N>
+__device__ __forceinline__ void pk_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 0 .. 63");
+  __builtin_amdgcn_s_waitcnt(((N & 15) | ((N >> 4) << 14)) | 0x0F70);
+}
+
+// The NSLOT x slots of one wave, each in its own __shared__ array: the compiler tracks the
+// direct-to-LDS loads per array, so a read of one slot waits only for that slot's loads.
+template <int NSLOT>
+struct PkSlots {
+  char* p[NSLOT];
+};
+
+// NL adjacent leaves of one lane's column (block s of leaf q at base + s * slab + q * lstride,
+// + lane * 16), AHEAD blocks in flight.  Issue order: blocks 0 .. AHEAD-1 (weights, then x) up
+// front; in iteration s the weights of block s + AHEAD before block s is consumed and its x into
+// the slot block s has just freed after.  x slots: AHEAD of them, block s in slot s % AHEAD.
+template <int SHAPE, int G, int NL, int AHEAD, typename V, int NA>
+__device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* base, int64_t slab, int lstride,
+                                               int lane, __amdgpu_buffer_rsrc_t xrs,
+                                               const uint32_t (&xvoff)[PkMf<SHAPE, G>::NI],
+                                               const PkSlots<AHEAD>& slots, float sc) {
+  using S = PkMf<SHAPE, G>;
+  static_assert(NA == S::NA, "accumulators a leaf");
+  static_assert(AHEAD >= 1 && AHEAD <= PK_BLOCKS, "blocks in flight");
+  constexpr int MR = S::MR;
+  constexpr int RING = AHEAD + 1 < PK_BLOCKS ? AHEAD + 1 : PK_BLOCKS;  // weight registers
+  constexpr int LPG = S::NI + NL;                                    // loads a block
+  auto block_rs = [&](int s) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + s * slab, (short)0, 0x7FFFFFFF, RSRC_WORD3);
+  };
+  u4 ring[RING][NL];
+  auto issue_w = [&](int s) {
+#pragma unroll
+    for (int q = 0; q < NL; ++q)
+      ring[s % RING][q] = __builtin_amdgcn_raw_buffer_load_b128(block_rs(s), lane * 16, q * lstride, PK_AUX);
+  };
+  auto issue_x = [&](auto SC) {
+    constexpr int s = decltype(SC)::value;
+#pragma unroll
+    for (int h = 0; h < S::NI; ++h) {
+#if defined(__HIP_DEVICE_COMPILE__)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_vptr)(slots.p[s % AHEAD] + h * 1024), 16, xvoff[h], 64 * s,
+                                               0, 0);
+#endif
+    }
+  };
+  pk_static_for<0, AHEAD>([&](auto SC) {
+    issue_w(decltype(SC)::value);
+    issue_x(SC);
+  });
+  // the x row this lane feeds in accumulator group gg
+  int xrow[NA];
+#pragma unroll
+  for (int gg = 0; gg < NA; ++gg) xrow[gg] = SHAPE == 16 ? (lane & 15) : 4 * gg + (lane & 3);
+
+  pk_static_for<0, PK_BLOCKS>([&](auto SC) {
+    constexpr int s = decltype(SC)::value;
+    if constexpr (s + AHEAD < PK_BLOCKS) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue_w(s + AHEAD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // block s landed, its x included; the loads issued after its x stay in flight
+    constexpr int full = PK_BLOCKS - 1 - s < AHEAD - 1 ? PK_BLOCKS - 1 - s : AHEAD - 1;
+    constexpr int after = full * LPG + (s + AHEAD < PK_BLOCKS ? NL : 0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    pk_wait_vm<after>();
+    __builtin_amdgcn_sched_barrier(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const char* slot = slots.p[s % AHEAD];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      f4 xq[NL][NA];
+#pragma unroll
+      for (int q = 0; q < NL; ++q)
+#pragma unroll
+        for (int gg = 0; gg < NA; ++gg) {
+          const int r = xrow[gg];
+          xq[q][gg] = *reinterpret_cast<const f4*>(slot + (q * 4 * MR + r * 4 + (v ^ pk_xsw(r))) * 16);
+        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = 4 * v + i;  // byte of the chunk: row 16 s + b of the leaf
+#pragma unroll
+        for (int q = 0; q < NL; ++q) {
+          const uint32_t u = ring[s % RING][q][b >> 2];
+          // f32(code) * scale, one rounding (the scale flushed on input by MODE.FP_DENORM = 2)
+          const float w = (float)((int32_t)(u << (24 - 8 * (b & 3))) >> 24) * sc;
+#pragma unroll
+          for (int gg = 0; gg < NA; ++gg) {
+            const V c = (s == 0 && b == 0) ? V{} : acc[q][gg];
+            if constexpr (SHAPE == 16) acc[q][gg] = __builtin_amdgcn_mfma_f32_16x16x1f32(xq[q][gg][i], w, c, 0, 0, 0);
+            else acc[q][gg] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq[q][gg][i], w, c, 0, 0, 0);
+          }
+        }
+      }
+    }
+    if constexpr (s + AHEAD < PK_BLOCKS) {
+      // the slot's reads above have returned (their values fed the instructions)
+      __builtin_amdgcn_sched_barrier(0);
+      issue_x(std::integral_constant<int, s + AHEAD>{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  });
+}
+
+template <int SHAPE, int G, int WAVES, int AHEAD>
+__global__ void __launch_bounds__(64 * WAVES) gemv_packed_mfma_kernel(GemvArgs g, const float* __restrict__ x) {
+  using S = PkMf<SHAPE, G>;
+  using V = PkV<SHAPE>;
+  constexpr int MR = S::MR;
+  constexpr int LEAVES = 2 * WAVES;
+  // x slots: one __shared__ array each (unused ones 16 bytes)
+  constexpr int SL = WAVES * S::SLOT;
+  __shared__ __attribute__((aligned(1024))) char xs0[AHEAD > 0 ? SL : 16];
+  __shared__ __attribute__((aligned(1024))) char xs1[AHEAD > 1 ? SL : 16];
+  __shared__ __attribute__((aligned(1024))) char xs2[AHEAD > 2 ? SL : 16];
+  __shared__ __attribute__((aligned(1024))) char xs3[AHEAD > 3 ? SL : 16];
+  __shared__ __attribute__((aligned(1024))) char xs4[AHEAD > 4 ? SL : 16];
+  __shared__ __attribute__((aligned(1024))) char xs5[AHEAD > 5 ? SL : 16];
+  __shared__ __attribute__((aligned(1024))) char xs6[AHEAD > 6 ? SL : 16];
+  __shared__ __attribute__((aligned(1024))) char xs7[AHEAD > 7 ? SL : 16];
+  __shared__ __attribute__((aligned(16))) float part[WAVES][MR][PK_COLS];
+  __shared__ unsigned int last_flag;
+
+  set_flush_inputs_mode();
+  gv_fetch_args(g, x);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the grid holds at most INT32_MAX workgroups (the host refuses more): a 32-bit split
+  const int64_t cg = blockIdx.x % (uint32_t)g.ncg;
+  const int64_t grp = blockIdx.x / (uint32_t)g.ncg;
+  const int64_t t0 = grp * LEAVES + 2 * wave;  // this wave's first leaf
+  const int m = (int)g.m;
+
+  V y[S::NA];
+#pragma unroll
+  for (int gg = 0; gg < S::NA; ++gg) y[gg] = V{};
+
+  if (t0 < g.nleaves) {
+    const int64_t j = cg * PK_COLS + lane;
+    const float sc = g.scales[j < g.n ? j : g.n - 1];  // columns past n are never stored
+    const int64_t slab = g.nleaves * g.ncg * 1024;
+    const int lstride = (int)(g.ncg * 1024);
+    const char* base = static_cast<const char*>(g.w) + (t0 * g.ncg + cg) * 1024;
+    // x: one resource over the whole operand (rows past m read row m - 1; the host keeps
+    // m * k * 4 < 2^31), this lane's chunk of each of a block's loads at a fixed offset, the
+    // block's first step in the scalar offset
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, (int)(g.m * g.k * 4), RSRC_WORD3);
+    uint32_t xvoff[S::NI];
+#pragma unroll
+    for (int h = 0; h < S::NI; ++h) {
+      const int c = (h * 64 + lane) % S::CHUNKS;
+      const int q = c / (4 * MR), r = (c >> 2) % MR, u = (c & 3) ^ pk_xsw(r);
+      const int64_t row = r < m ? r : m - 1;
+      xvoff[h] = (uint32_t)((row * g.k + (t0 + q) * GV_CH + 4 * u) * 4);
+    }
+    PkSlots<AHEAD> slots;
+    char* all[8] = {xs0, xs1, xs2, xs3, xs4, xs5, xs6, xs7};
+#pragma unroll
+    for (int i = 0; i < AHEAD; ++i) slots.p[i] = all[i] + wave * S::SLOT;
+    if (t0 + 1 < g.nleaves) {
+      V acc[2][S::NA];
+      pk_leaves_mfma<SHAPE, G, 2, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, slots, sc);
+#pragma unroll
+      for (int gg = 0; gg < S::NA; ++gg) y[gg] = acc[0][gg] + acc[1][gg];  // the level-1 pair
+    } else {
+      V acc[1][S::NA];
+      pk_leaves_mfma<SHAPE, G, 1, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, slots, sc);
+#pragma unroll
+      for (int gg = 0; gg < S::NA; ++gg) y[gg] = acc[0][gg];  // the odd last leaf, carried
+    }
+  }
+
+  if constexpr (SHAPE == 16) {
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[wave][4 * (lane >> 4) + i][16 * blk + (lane & 15)] = y[0][4 * blk + i];
+  } else {
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[wave][4 * gg + r][lane] = y[gg][r];
+  }
+  gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, true>(g, part, last_flag, tid, grp, cg, m);
+}
+
+template <int SHAPE, int G>
+static hipError_t launch_pkmf(const GemvArgs& g, const float* x, int waves, dim3 grid, hipStream_t s) {
+  switch (waves) {
+    case PK_WAVES_WHOLE:
+      hipLaunchKernelGGL((gemv_packed_mfma_kernel<SHAPE, G, PK_WAVES_WHOLE, PK_AHEAD>), grid,
+                         dim3(64 * PK_WAVES_WHOLE), 0, s, g, x);
+      break;
+    case PK_WAVES_SPLIT:
+      hipLaunchKernelGGL((gemv_packed_mfma_kernel<SHAPE, G, PK_WAVES_SPLIT, PK_BLOCKS>), grid,
+                         dim3(64 * PK_WAVES_SPLIT), 0, s, g, x);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_packed_mfma(const GemvArgs& g, const float* x, int waves, dim3 grid, hipStream_t stream) {
+  if (g.m <= 4) return launch_pkmf<4, 1>(g, x, waves, grid, stream);
+  if (g.m <= 8) return launch_pkmf<4, 2>(g, x, waves, grid, stream);
+  return launch_pkmf<16, 1>(g, x, waves, grid, stream);
+}
+
 hipError_t launch_int8w_pack(void* dst, const void* codes, int64_t k, int64_t n, hipStream_t stream) {
   const int64_t P = k / GV_CH, ncg = (n + PK_COLS - 1) / PK_COLS;
   const int64_t chunks = PK_BLOCKS * P * ncg * 64;

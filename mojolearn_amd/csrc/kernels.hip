@@ -324,13 +324,20 @@ hipError_t run_gemm(const GemmProblem& p, float* ws, int num_cus, hipStream_t st
 
 static int64_t pk_groups(int64_t n) { return (n + PK_GROUP_COLS - 1) / PK_GROUP_COLS; }
 
-// Waves a workgroup of the packed product: for the decode rows (m <= 2; more rows would spill
-// the x values a 16-wave workgroup keeps in scalar registers) the whole-column workgroups (32
-// leaves) when the launch still holds a workgroup for three of every four CUs, else 4-leaf groups.
-static int pk_waves(int64_t m, int64_t n, int64_t k, int num_cus) {
+// The packed product on the matrix cores: 3 <= m <= 16, x on the 16-byte grid (its blocks are
+// loaded straight into LDS in 16-byte chunks) and addressed in 31 bits.
+static bool pk_mfma(int64_t m, int64_t k, const float* x) {
+  return m >= PK_MFMA_MIN_M && m <= GV_MAXM && aligned(x, 16) && m * k * 4 <= INT32_MAX;
+}
+
+// Waves a workgroup of the packed product: the whole-column workgroups (32 leaves) when the
+// launch still holds a workgroup for three of every four CUs, else 4-leaf groups.  The VALU
+// kernel takes whole columns only for the decode rows (m <= 2: more rows would spill the x
+// values a 16-wave workgroup keeps in scalar registers); the matrix-core one at every m.
+static int pk_waves(int64_t m, int64_t n, int64_t k, bool mfma, int num_cus) {
   const int64_t P = k / GV_CH, whole = 2 * PK_WAVES_WHOLE;
   const bool fills = pk_groups(n) * ((P + whole - 1) / whole) * 4 >= 3 * (int64_t)num_cus;
-  return m <= 2 && fills ? PK_WAVES_WHOLE : PK_WAVES_SPLIT;
+  return (m <= 2 || mfma) && fills ? PK_WAVES_WHOLE : PK_WAVES_SPLIT;
 }
 
 static int64_t pk_ngroups(int64_t k, int waves) { return (k / GV_CH + 2 * waves - 1) / (2 * waves); }
@@ -370,7 +377,8 @@ std::string gemv_packed_limit(int64_t m, int64_t n, int64_t k, const void* packe
 hipError_t run_gemv_packed(float* c, const float* x, const void* packed, const float* scales, const float* bias,
                            int64_t m, int64_t n, int64_t k, float* ws, int num_cus, hipStream_t stream) {
   if (!gemv_packed_limit(m, n, k, packed).empty() || !c || !x || !packed || !scales) return hipErrorInvalidValue;
-  const int waves = pk_waves(m, n, k, num_cus);
+  const bool mfma = pk_mfma(m, k, x);
+  const int waves = pk_waves(m, n, k, mfma, num_cus);
   GemvArgs v;
   v.c = c; v.w = packed; v.scales = scales; v.bias = bias;
   v.m = m; v.n = n; v.k = k; v.leaf = GV_CH; v.nleaves = k / GV_CH; v.ncg = pk_groups(n);
@@ -378,7 +386,8 @@ hipError_t run_gemv_packed(float* c, const float* x, const void* packed, const f
   v.counter = reinterpret_cast<unsigned int*>(ws);
   v.ws = ws ? ws + round_floats(gemv_packed_counter_count(m, n, k)) : nullptr;
   if (v.ngroups > 1 && ws == nullptr) return hipErrorInvalidValue;
-  return launch_gemv_packed(v, x, waves, dim3((unsigned)(v.ncg * v.ngroups)), stream);
+  const dim3 grid((unsigned)(v.ncg * v.ngroups));
+  return mfma ? launch_gemv_packed_mfma(v, x, waves, grid, stream) : launch_gemv_packed(v, x, waves, grid, stream);
 }
 
 // Zero `count` 32-bit words (the completion counters of a skinny product) with a kernel: a

@@ -4,11 +4,12 @@
   [leaf][block][row][group][lane] and a transpose to [block][leaf][group][lane][row], columns
   padded with zero codes), which shares no index arithmetic with the kernel.
 * The packed decode product is bit-equal, on poisoned outputs, to the oracle and to the
-  row-major product (gemm_int8w) for 1 <= m <= 16: whole-column workgroups (32 leaves, one
-  group), whole-column workgroups with a ragged second group and an odd last leaf, 4-leaf
-  groups folded across workgroups, ragged column groups, special x values, extreme and
-  subnormal scales, with and without the fused bias; again on a second call (counters left
-  zero).
+  row-major product (gemm_int8w) for 1 <= m <= 16, on the VALU kernel (m <= 2, or x off the
+  16-byte grid) and the matrix-core one (3 <= m <= 16, both shapes): whole-column workgroups
+  (32 leaves, one group), whole-column workgroups with a ragged second group and an odd last
+  leaf, 4-leaf groups folded across workgroups, ragged column groups, special x values,
+  extreme and subnormal scales, with and without the fused bias; again on a second call
+  (counters left zero).
 * A PackedPlan captured in a HIP graph on a fresh stream replays correctly with eager work in
   between.
 """
@@ -61,12 +62,15 @@ def _x(rng, m, k, special):
     return x
 
 
-# whole-column workgroups where m <= 2 and ceil(n / 64) * ceil(k / 4096) >= 192 (on 256 CUs):
-# 1x14336x4096 (one group), 1x8196x4480 and 2x12300x4224 (a second group of 3 or 1 leaves: an
-# odd last leaf run alone); the rest in 4-leaf groups
+# whole-column workgroups where ceil(n / 64) * ceil(k / 4096) >= 192 (on 256 CUs) and m <= 2
+# (the VALU kernel) or 3 <= m <= 16 with x on the 16-byte grid (the matrix-core kernel):
+# 1x14336x4096, 5x14336x4096, 16x12288x4096 (one group), 1x8196x4480, 8x8196x4480,
+# 16x8196x4480, 2x12300x4224 and 3x12300x4224 (a second group of 3 or 1 leaves: an odd last
+# leaf run alone); the rest in 4-leaf groups
 PACKED_SHAPES = [(1, 14336, 4096), (2, 300, 640), (1, 1, 128), (1, 130, 256), (3, 257, 1024), (4, 1000, 4096),
                  (8, 64, 1152), (16, 129, 1152), (16, 2048, 4096), (1, 8196, 4480), (2, 4096, 8192), (5, 14336, 4096),
-                 (16, 12288, 4096), (2, 12300, 4224), (1, 1792, 4096), (1, 64, 384)]
+                 (16, 12288, 4096), (2, 12300, 4224), (1, 1792, 4096), (1, 64, 384), (4, 14336, 4096),
+                 (8, 8196, 4480), (16, 8196, 4480), (3, 12300, 4224), (12, 14336, 4096)]
 
 
 @pytest.mark.parametrize("shape", PACKED_SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in PACKED_SHAPES])
@@ -98,6 +102,28 @@ def test_packed_gemv_parity(oracle, shape):
         assert bad.size == 0, f"call {call}: {bad.size} words differ, first at {divmod(int(bad[0]), n)}"
     rowmajor = D.gemm_int8w(tx, tc, ts, bias=tb).cpu().numpy()
     assert np.array_equal(_bits(rowmajor), _bits(got))
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 14336, 4096), (8, 300, 1024), (16, 12288, 4096)])
+def test_packed_gemv_x_off_the_16_byte_grid(oracle, m, n, k):
+    """x at a 4-byte offset: the matrix-core kernel loads x in 16-byte chunks, so these products
+    take the VALU kernel (whole columns or 4-leaf groups); the bits are the same."""
+    from mojolearn_amd import device as D
+    rng = np.random.default_rng(m + n + k + 5)
+    x = _x(rng, m, k, True)
+    codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
+    scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    print(f"packed gemv, x off the grid: m={m} n={n} k={k}", flush=True)
+    store = torch.empty(m * k + 1, dtype=torch.float32, device=DEV)
+    tx = store[1:].view(m, k)
+    tx.copy_(_t(x))
+    packed = D.pack_int8w(_t(codes))
+    want = oracle.nan_canon(oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0))
+    out = torch.full((m, n), POISON, dtype=torch.float32, device=DEV)
+    D.gemv_int8w_packed(tx, packed, _t(scales), out=out)
+    torch.cuda.synchronize()
+    bad = np.flatnonzero(_bits(out.cpu().numpy()) != _bits(want))
+    assert bad.size == 0, f"{bad.size} words differ, first at {divmod(int(bad[0]), n)}"
 
 
 def test_packed_plan_captured_on_a_fresh_stream(oracle):
