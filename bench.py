@@ -201,9 +201,11 @@ def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=N
 
 def bench_read_floor(torch, steps, warmup, runs, nbuf=8):
     """The memory floors of the decode GEMV's weight stream: a read-only pass over the same
-    rotating int8 W[4096x14336] buffers, (linear) in address order with 16-byte loads, and
-    (leaf) in the decode kernel's own order -- a wave per 128-row leaf and 256-byte strip, every
-    leaf of a column streamed at once, as the contract's leaf chains require."""
+    rotating int8 W[4096x14336] buffers, (linear) in address order with 16-byte loads, (leaf) in
+    the row-major decode kernel's own order -- a wave per 128-row leaf and 256-byte strip, every
+    leaf of a column streamed at once, as the contract's leaf chains require -- and (packed) in
+    the decode-packed product's order: whole-column workgroups of 16 waves, two leaves a wave,
+    block s of every leaf read together."""
     from mojolearn_amd import _native
     L = _native.lib()
     k, n = 4096, 14336
@@ -212,7 +214,7 @@ def bench_read_floor(torch, steps, warmup, runs, nbuf=8):
     bufs = [torch.randint(-127, 128, (k, n), dtype=torch.int8, device="cuda:0", generator=gen) for _ in range(nbuf)]
     sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
     res = {}
-    for pattern, name in ((0, "linear"), (1, "leaf")):
+    for pattern, name in ((0, "linear"), (1, "leaf"), (2, "packed")):
         calls = [lambda s, b=b, pattern=pattern: _native.check(
             L.mlg_stream_read(b.data_ptr(), k, n, pattern, sink.data_ptr(), s.cuda_stream)) for b in bufs]
         r = _timed(calls, max(steps, 2 * nbuf), warmup, torch, runs)

@@ -771,7 +771,7 @@ int mlg_stream_read(const void* w, int64_t rows, int64_t cols, int32_t pattern, 
   return guarded([&] {
     hip_check(mlg::run_stream_read(w, rows, cols, pattern, sink, static_cast<hipStream_t>(stream)),
               "stream_read launch (pattern 0: 16-byte aligned, 16-byte multiple; pattern 1: rows a "
-              "multiple of 512, cols of 256)");
+              "multiple of 512, cols of 256; pattern 2: rows a multiple of 4096, cols of 64, below 2^31 bytes)");
   });
 }
 

@@ -86,7 +86,8 @@ std::string gemv_packed_limit(int64_t m, int64_t n, int64_t k, const void* packe
 hipError_t run_gemv_packed(float* c, const float* x, const void* packed, const float* scales, const float* bias,
                            int64_t m, int64_t n, int64_t k, float* ws, int num_cus, hipStream_t stream);
 // Read-only streams over an int8 matrix W[rows][cols] (stream_read.hip): pattern 0 the whole
-// matrix in address order, pattern 1 the decode kernel's leaf-by-leaf reads.  Measurement only.
+// matrix in address order, pattern 1 the row-major decode kernel's leaf-by-leaf reads, pattern 2
+// the decode-packed product's whole-column reads.  Measurement only.
 hipError_t run_stream_read(const void* w, int64_t rows, int64_t cols, int pattern, uint32_t* sink,
                            hipStream_t stream);
 

@@ -30,8 +30,9 @@ def test_library_exports_every_declared_symbol():
 
 def test_stream_read_refuses_before_any_launch():
     """The read-floor entry (bench.py --read-floor) checks its shapes on the host: a missing
-    pointer, an unknown pattern, or a leaf pattern whose rows are not whole groups of four
-    128-row leaves is refused with a message and launches nothing."""
+    pointer, an unknown pattern, a leaf pattern whose rows are not whole groups of four
+    128-row leaves, or a packed pattern whose rows are not whole 32-leaf groups (or whose
+    columns are not whole 64-column groups) is refused with a message and launches nothing."""
     L = _native.lib()
     sink = ctypes.c_uint32(0)
     assert L.mlg_stream_read(None, 4096, 14336, 0, ctypes.addressof(sink), None) == 1
@@ -39,6 +40,8 @@ def test_stream_read_refuses_before_any_launch():
     buf = (ctypes.c_uint8 * 16)()
     assert L.mlg_stream_read(ctypes.addressof(buf), 100, 256, 1, ctypes.addressof(sink), None) == 1
     assert L.mlg_stream_read(ctypes.addressof(buf), 512, 256, 7, ctypes.addressof(sink), None) == 1
+    assert L.mlg_stream_read(ctypes.addressof(buf), 2048, 256, 2, ctypes.addressof(sink), None) == 1
+    assert L.mlg_stream_read(ctypes.addressof(buf), 4096, 100, 2, ctypes.addressof(sink), None) == 1
 
 
 def test_int8w_packed_sizes_and_refusals():
