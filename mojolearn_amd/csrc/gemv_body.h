@@ -358,19 +358,21 @@ __device__ __forceinline__ void gv_fold_pow2(const GemvArgs& g, int tid, int64_t
 // then either the store (one group) or the count and, in the workgroup that completes it,
 // the fold of every group's root (the rest of the contract's tree), bias and store.
 //
-// PAIRED: each wave ran two adjacent leaves and wrote their level-1 node (the pair's sum, or the
-// odd last leaf carried), so part holds LEAVES / 2 nodes -- the tree over them is the rest of the
-// contract's tree over the workgroup's leaves.
-template <int MR, int COLS, int LEAVES = GV_LEAVES, int THREADS = GV_THREADS, bool PAIRED = false>
-__device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[PAIRED ? LEAVES / 2 : LEAVES][MR][COLS],
+// LPN (leaves per node) 2 or 4: each wave ran LPN adjacent leaves (an aligned subtree) and
+// wrote that subtree's node -- for the last, partial subtree the contract's tree over the leaves
+// it has, the odd one carried -- so part holds LEAVES / LPN nodes, and the tree over them is the
+// rest of the contract's tree over the workgroup's leaves.
+template <int MR, int COLS, int LEAVES = GV_LEAVES, int THREADS = GV_THREADS, int LPN = 1>
+__device__ __forceinline__ void gv_finish(const GemvArgs& g, float (&part)[LEAVES / LPN][MR][COLS],
                                           unsigned int& last_flag, int tid, int64_t grp, int64_t cg, int m) {
-  constexpr int NODES = PAIRED ? LEAVES / 2 : LEAVES;
+  constexpr int NODES = LEAVES / LPN;
+  static_assert(LPN == 1 || LPN == 2 || LPN == 4, "a node is a subtree of 1, 2 or 4 leaves");
   static_assert(NODES == 2 || NODES == 4 || NODES == 8 || NODES == 16, "a workgroup folds 2 .. 16 nodes");
-  static_assert(PAIRED || LEAVES == 4 || LEAVES == 8, "unpaired workgroups fold 4 or 8 leaves");
+  static_assert(LPN > 1 || LEAVES == 4 || LEAVES == 8, "workgroups of single-leaf nodes fold 4 or 8 leaves");
   __syncthreads();
   const int64_t left = g.nleaves - grp * LEAVES;
   const int cntl = left < LEAVES ? (int)left : LEAVES;
-  const int cnt = PAIRED ? (cntl + 1) / 2 : cntl;  // nodes written
+  const int cnt = (cntl + LPN - 1) / LPN;  // nodes written
   constexpr int CPT = (MR * COLS + THREADS - 1) / THREADS;  // cells per thread
   constexpr int LB = CPT < 4 ? CPT : 4;                      // cells per batch of LDS reads
   // this thread's cells tid + c * THREADS of rows < m, LB at a time: every partial of a

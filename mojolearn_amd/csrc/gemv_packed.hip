@@ -18,7 +18,7 @@
 // are packed as zero codes and never stored.  The arithmetic and its order are gemv_nn_kernel's:
 // per leaf the chain acc = fma(x, f32(code) * scale, acc) in step order from +0, the level-1
 // pair of a wave's two leaves added in registers, the rest of the tree over the workgroup's
-// pairs (gv_finish, PAIRED), and past 32 leaves the group roots folded by the workgroup that
+// pairs (gv_finish with two-leaf nodes), and past 32 leaves the group roots folded by the workgroup that
 // completes the count -- so the bits are the row-major product's.
 #include "gemv_body.h"
 
@@ -181,7 +181,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
 
 #pragma unroll
   for (int r = 0; r < MR; ++r) part[wave][r][lane] = y[r];
-  gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, true>(g, part, last_flag, tid, grp, cg, m);
+  gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, 2>(g, part, last_flag, tid, grp, cg, m);
 }
 
 // ---- 3 <= m <= 16 on the matrix cores, from the decode-packed layout.
@@ -416,7 +416,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_mfma_kernel(GemvArgs g
 #pragma unroll
       for (int r = 0; r < 4; ++r) part[wave][4 * gg + r][lane] = y[gg][r];
   }
-  gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, true>(g, part, last_flag, tid, grp, cg, m);
+  gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, 2>(g, part, last_flag, tid, grp, cg, m);
 }
 
 template <int SHAPE, int G>
