@@ -11,6 +11,8 @@ mismatching words against the CPU oracle over every output cell (the output firs
 poison word), and the CPU baseline timed on the host cores: the scalar oracle on one thread on
 the reference's host-capped block (the headline `cpu_baseline`) and the reference's fast CPU
 column restated on every thread (with --all, both arms on every workload, and the host's CPU).
+Before the headline's W warmup steps the product runs untimed for CLOCK_RAMP_S seconds, which
+brings the engine clock to its steady state under this load; the K timed steps are unchanged.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
 """
@@ -76,6 +78,27 @@ def graph_time(calls, steps, warmup, torch):
     return graph_runs(calls, steps, warmup, torch)[0]
 
 
+#: seconds of untimed launches before the headline's warmup steps: the engine clock's ramp to its
+#: steady state under this load.  Measured with 20 timed steps after 5 warmup launches, the first
+#: timed run: 113.5 TFLOP/s with no ramp, 119-120 after 0.25 s, 123.5 after 1 s (the same kernel at
+#: a lower clock; 123-124 in steady state).
+CLOCK_RAMP_S = 1.0
+
+
+def clock_ramp(calls, torch, seconds=CLOCK_RAMP_S):
+    """Untimed launches of `calls` on a private stream until `seconds` of wall time have passed;
+    the number of launches."""
+    s = torch.cuda.Stream()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        with torch.cuda.stream(s):
+            for i in range(16):
+                calls[i % len(calls)](s)
+        s.synchronize()
+        n += 16
+    return n
+
+
 def _timed(calls, steps, warmup, torch, runs, eager=None):
     """{"ms": ...} from one run, or with runs > 1 the median run and the fastest and slowest."""
     t = sorted(graph_runs(calls, steps, warmup, torch, runs, eager))
@@ -118,14 +141,16 @@ def _t(torch, x):
     return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
 
 
-def bench_prefill(torch, D, W, O, steps, warmup, check, runs=1, cols=None):
+def bench_prefill(torch, D, W, O, steps, warmup, check, runs=1, cols=None, ramp=False):
     """The prefill projection; `cols` keeps W's and bias's first columns (one GPU's column
-    shard at its real shape)."""
+    shard at its real shape); `ramp`: clock_ramp before the warmup steps."""
     x, w, bias = W.prefill()
     if cols is not None:
         w, bias = np.ascontiguousarray(w[:, :cols]), np.ascontiguousarray(bias[:cols])
     plan = D.Plan(_t(torch, x), _t(torch, w), bias=_t(torch, bias))
+    ramped = clock_ramp([plan], torch) if ramp else 0
     res = _timed([plan], steps, warmup, torch, runs)
+    res["ramp_launches"] = ramped
     res["out"] = None
     ms = res["ms"]
     m, k = x.shape
@@ -657,7 +682,7 @@ def main():
     from oracle import oracle as O
 
     check = not args.no_check
-    pre = bench_prefill(torch, D, W, O, args.steps, args.warmup, check)
+    pre = bench_prefill(torch, D, W, O, args.steps, args.warmup, check, ramp=True)
     gpu_out = pre.pop("out")
     extra = {}
     if args.all:
@@ -711,6 +736,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "untimed_clock_ramp": {"seconds": CLOCK_RAMP_S, "launches": pre["ramp_launches"]},
         "ms_per_step": round(pre["ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
