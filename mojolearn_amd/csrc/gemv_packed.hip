@@ -194,27 +194,42 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
 //    4 blk + i, row 4 (l / 16) + i of column 16 blk + l % 16;
 //  * SHAPE 4 (v_mfma_f32_4x4x1_16b_f32, 3 <= m <= 8, G groups of four rows): lane l feeds row
 //    4 g + l % 4 and gets back, in register r, row 4 g + r of its own column.
-// A wave runs two adjacent leaves, one instruction per leaf per step.  x travels through LDS:
-// each wave streams the x values of its leaves' next blocks (MR rows by 16 steps a leaf) into a
-// ring of its own LDS slots with direct-to-LDS loads, issued with the block's weights, and reads
-// them back four steps at a time.  The workgroup and its fold are gemv_packed_kernel's.
+// A wave runs two adjacent leaves, one instruction per leaf per step.  Only one lane group
+// needs each x value: the instruction's A broadcast (CBSZ, ABID) feeds every block from block
+// ABID's lanes.  So the lanes hold different steps of x: with SHAPE 16, lane 16u + r holds
+// x[r][steps 4u .. 4u+3 of the block] of one leaf (one 16-byte read a leaf a block, block u
+// broadcast for steps 4u .. 4u+3); with SHAPE 4, lane 32g + 16q + 4u + r holds x[4g + r][steps
+// 4u .. 4u+3] of leaf q (one read a block for both leaves and both groups, block 8g + 4q + u
+// broadcast).  x travels through LDS: each wave streams its leaves' x for the next blocks into a
+// ring of its own LDS slots with direct-to-LDS loads, issued with the block's weights, lane L's
+// chunk at L * 16.  The workgroup and its fold are gemv_packed_kernel's.
 template <int SHAPE, int G>
 struct PkMf {
-  static constexpr int MR = SHAPE == 16 ? 16 : 4 * G;     // rows the lane's instructions cover
-  static constexpr int NA = SHAPE == 16 ? 1 : G;           // accumulators a leaf
-  static constexpr int CHUNKS = 2 * MR * 4;                // 16-byte x chunks a block: 2 leaves, MR rows, 16 steps
-  static constexpr int NI = CHUNKS < 64 ? 1 : CHUNKS / 64;  // direct-to-LDS loads a block
-  static constexpr int SLOT = NI * 1024;                   // bytes of one ring slot
+  static constexpr int MR = SHAPE == 16 ? 16 : 4 * G;  // rows the lane's instructions cover
+  static constexpr int NA = SHAPE == 16 ? 1 : G;        // accumulators a leaf
+  static constexpr int NI = SHAPE == 16 ? 2 : 1;        // x loads (and reads) a block, 1 KB each
+  static constexpr int SLOT = NI * 1024;                // bytes of one ring slot
 };
 typedef float pk_v16f __attribute__((ext_vector_type(16)));
 typedef float pk_v4f __attribute__((ext_vector_type(4)));
 template <int SHAPE>
 using PkV = typename std::conditional<SHAPE == 16, pk_v16f, pk_v4f>::type;
 
-// Chunk c of a slot holds x[r][leaf q, steps 4 u .. 4 u + 3 of the block] with q = c / (4 MR),
-// r = (c / 4) % MR and u = (c % 4) ^ pk_xsw(r): the sixteen rows one read serves land in
-// different LDS banks.
-__device__ __forceinline__ int pk_xsw(int r) { return (r >> 2) & 3; }
+// The x chunk lane l of load h holds: leaf q, row r, steps 4u .. 4u+3 of the block (the
+// broadcast layout above; with one group of four rows, lanes 32 .. 63 repeat lanes 0 .. 31).
+template <int SHAPE, int G>
+__device__ __forceinline__ void pk_xchunk(int h, int lane, int& q, int& r, int& u) {
+  if constexpr (SHAPE == 16) {
+    q = h;
+    r = lane & 15;
+    u = lane >> 4;
+  } else {
+    const int l = G == 1 ? (lane & 31) : lane;
+    q = (l >> 4) & 1;
+    u = (l >> 2) & 3;
+    r = 4 * (l >> 5) + (l & 3);
+  }
+}
 
 // f(integral_constant<int, I>) for I = B .. E-1: the block loop with its index a constant, so
 // every wait count and LDS slot below is named at compile time.
@@ -278,10 +293,6 @@ __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* bas
     issue_w(decltype(SC)::value);
     issue_x(SC);
   });
-  // the x row this lane feeds in accumulator group gg
-  int xrow[NA];
-#pragma unroll
-  for (int gg = 0; gg < NA; ++gg) xrow[gg] = SHAPE == 16 ? (lane & 15) : 4 * gg + (lane & 3);
 
   pk_static_for<0, PK_BLOCKS>([&](auto SC) {
     constexpr int s = decltype(SC)::value;
@@ -298,33 +309,26 @@ __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* bas
     __builtin_amdgcn_sched_barrier(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const char* slot = slots.p[s % AHEAD];
+    f4 xq[S::NI];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      f4 xq[NL][NA];
-#pragma unroll
-      for (int q = 0; q < NL; ++q)
-#pragma unroll
-        for (int gg = 0; gg < NA; ++gg) {
-          const int r = xrow[gg];
-          xq[q][gg] = *reinterpret_cast<const f4*>(slot + (q * 4 * MR + r * 4 + (v ^ pk_xsw(r))) * 16);
-        }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int b = 4 * v + i;  // byte of the chunk: row 16 s + b of the leaf
-#pragma unroll
-        for (int q = 0; q < NL; ++q) {
-          const uint32_t u = ring[s % RING][q][b >> 2];
-          // f32(code) * scale, one rounding (the scale flushed on input by MODE.FP_DENORM = 2)
-          const float w = (float)((int32_t)(u << (24 - 8 * (b & 3))) >> 24) * sc;
-#pragma unroll
-          for (int gg = 0; gg < NA; ++gg) {
-            const V c = (s == 0 && b == 0) ? V{} : acc[q][gg];
-            if constexpr (SHAPE == 16) acc[q][gg] = __builtin_amdgcn_mfma_f32_16x16x1f32(xq[q][gg][i], w, c, 0, 0, 0);
-            else acc[q][gg] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq[q][gg][i], w, c, 0, 0, 0);
-          }
-        }
-      }
-    }
+    for (int h = 0; h < S::NI; ++h) xq[h] = *reinterpret_cast<const f4*>(slot + h * 1024 + lane * 16);
+    pk_static_for<0, PK_RB>([&](auto BC) {
+      constexpr int b = decltype(BC)::value;  // byte of the chunk: row 16 s + b of the leaf
+      pk_static_for<0, NL>([&](auto QC) {
+        constexpr int q = decltype(QC)::value;
+        const uint32_t u = ring[s % RING][q][b >> 2];
+        // f32(code) * scale, one rounding (the scale flushed on input by MODE.FP_DENORM = 2)
+        const float w = (float)((int32_t)(u << (24 - 8 * (b & 3))) >> 24) * sc;
+        pk_static_for<0, NA>([&](auto GC) {
+          constexpr int gg = decltype(GC)::value;
+          const V c = (s == 0 && b == 0) ? V{} : acc[q][gg];
+          if constexpr (SHAPE == 16)  // block b / 4 holds x of steps 4 (b / 4) .. +3 of leaf q
+            acc[q][gg] = __builtin_amdgcn_mfma_f32_16x16x1f32(xq[q][b & 3], w, c, 2, b >> 2, 0);
+          else  // block 8 gg + 4 q + b / 4 holds rows 4 gg .. 4 gg + 3 of those steps
+            acc[q][gg] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq[0][b & 3], w, c, 4, 8 * gg + 4 * q + (b >> 2), 0);
+        });
+      });
+    });
     if constexpr (s + AHEAD < PK_BLOCKS) {
       // the slot's reads above have returned (their values fed the instructions)
       __builtin_amdgcn_sched_barrier(0);
@@ -383,8 +387,8 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_mfma_kernel(GemvArgs g
     uint32_t xvoff[S::NI];
 #pragma unroll
     for (int h = 0; h < S::NI; ++h) {
-      const int c = (h * 64 + lane) % S::CHUNKS;
-      const int q = c / (4 * MR), r = (c >> 2) % MR, u = (c & 3) ^ pk_xsw(r);
+      int q, r, u;
+      pk_xchunk<SHAPE, G>(h, lane, q, r, u);
       const int64_t row = r < m ? r : m - 1;
       xvoff[h] = (uint32_t)((row * g.k + (t0 + q) * GV_CH + 4 * u) * 4);
     }
