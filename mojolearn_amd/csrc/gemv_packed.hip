@@ -216,7 +216,8 @@ template <int SHAPE>
 using PkV = typename std::conditional<SHAPE == 16, pk_v16f, pk_v4f>::type;
 
 // The x chunk lane l of load h holds: leaf q, row r, steps 4u .. 4u+3 of the block (the
-// broadcast layout above; with one group of four rows, lanes 32 .. 63 repeat lanes 0 .. 31).
+// broadcast layout above; with one group of four rows, lanes 32 .. 63 load nothing and their
+// half of the slot is never read).
 template <int SHAPE, int G>
 __device__ __forceinline__ void pk_xchunk(int h, int lane, int& q, int& r, int& u) {
   if constexpr (SHAPE == 16) {
@@ -279,14 +280,17 @@ __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* bas
     for (int q = 0; q < NL; ++q)
       ring[s % RING][q] = __builtin_amdgcn_raw_buffer_load_b128(block_rs(s), lane * 16, q * lstride, PK_AUX);
   };
+  // (with one group of four rows only lanes 0 .. 31 load: the other half of the chunk would repeat them)
   auto issue_x = [&](auto SC) {
     constexpr int s = decltype(SC)::value;
 #pragma unroll
     for (int h = 0; h < S::NI; ++h) {
+      if (SHAPE == 16 || G == 2 || lane < 32) {
 #if defined(__HIP_DEVICE_COMPILE__)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_vptr)(slots.p[s % AHEAD] + h * 1024), 16, xvoff[h], 64 * s,
-                                               0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_vptr)(slots.p[s % AHEAD] + h * 1024), 16, xvoff[h], 64 * s,
+                                                 0, 0);
 #endif
+      }
     }
   };
   pk_static_for<0, AHEAD>([&](auto SC) {
