@@ -81,9 +81,10 @@ hipError_t launch_gemv_mfma_nn(const GemvArgs& g, const float* x, int b_type, di
 // 2 <= m <= 8 on the 4 x 4 shape (same conditions as the 16 x 16 kernel).
 hipError_t launch_gemv_mfma4_nn(const GemvArgs& g, const float* x, int b_type, int64_t m, dim3 grid,
                                 hipStream_t stream);
-// The decode-packed int8 layout (gemv_packed.hip): 64-column groups, two leaves a wave, `waves`
-// a workgroup: PK_WAVES_WHOLE (32 leaves, the whole tree at K = 4096) when the launch fills the
-// CUs, else PK_WAVES_SPLIT (4 leaves, group roots folded across workgroups).
+// The decode-packed int8 layout (gemv_packed.hip): 64-column groups, `waves` a workgroup:
+// PK_WAVES_WHOLE (16 waves of two leaves: 32 leaves, the whole tree at K = 4096) when the launch
+// fills the CUs, else 4-leaf groups whose roots fold across workgroups (PK_WAVES_SPLIT: two waves
+// of two leaves on the matrix cores, four waves of one leaf on the VALU).
 constexpr int PK_GROUP_COLS = 64;
 constexpr int PK_WAVES_WHOLE = 16;
 constexpr int PK_WAVES_SPLIT = 2;

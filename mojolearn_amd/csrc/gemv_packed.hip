@@ -131,12 +131,13 @@ __device__ __forceinline__ void gv_leaves_packed(float (&acc)[NL][MR], const cha
   }
 }
 
-// WAVES waves a workgroup, each running two adjacent leaves of the workgroup's 64 columns
-// (2 * WAVES leaves: an aligned subtree).  g.w is the packed buffer, g.nleaves = P, g.ncg the
-// column groups of 64.
-template <int MR, int WAVES, int AHEAD>
+// WAVES waves a workgroup, each running LPW adjacent leaves (two, or one when the launch is small
+// and shorter chains on more waves pay) of the workgroup's 64 columns (LPW * WAVES leaves: an
+// aligned subtree).  g.w is the packed buffer, g.nleaves = P, g.ncg the column groups of 64.
+template <int MR, int WAVES, int AHEAD, int LPW = 2>
 __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, const float* __restrict__ x) {
-  constexpr int LEAVES = 2 * WAVES;
+  static_assert(LPW == 1 || LPW == 2, "one or two leaves a wave");
+  constexpr int LEAVES = LPW * WAVES;
   __shared__ float part[WAVES][MR][PK_COLS];
   __shared__ unsigned int last_flag;
 
@@ -148,7 +149,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
   // the grid holds at most INT32_MAX workgroups (the host refuses more): a 32-bit split
   const int64_t cg = blockIdx.x % (uint32_t)g.ncg;
   const int64_t grp = blockIdx.x / (uint32_t)g.ncg;
-  const int64_t t0 = grp * LEAVES + 2 * wave;  // this wave's first leaf
+  const int64_t t0 = grp * LEAVES + LPW * wave;  // this wave's first leaf
   const int m = (int)g.m;
 
   float y[MR];
@@ -162,7 +163,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
     const int64_t slab = g.nleaves * g.ncg * 1024;  // bytes of one block of every leaf
     const int lstride = (int)(g.ncg * 1024);        // leaf t to t + 1 (the host keeps it < 2^31)
     const char* base = static_cast<const char*>(g.w) + (t0 * g.ncg + cg) * 1024;
-    if (t0 + 1 < g.nleaves) {
+    if (LPW == 2 && t0 + 1 < g.nleaves) {
       float acc[2][MR];
 #pragma unroll
       for (int r = 0; r < MR; ++r) acc[0][r] = acc[1][r] = 0.f;
@@ -175,13 +176,13 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
       for (int r = 0; r < MR; ++r) acc[0][r] = 0.f;
       gv_leaves_packed<MR, 1, AHEAD>(acc, base, slab, lstride, lane, x + t0 * GV_CH, g.k, m, sc);
 #pragma unroll
-      for (int r = 0; r < MR; ++r) y[r] = acc[0][r];  // the odd last leaf, carried
+      for (int r = 0; r < MR; ++r) y[r] = acc[0][r];  // one leaf, or the odd last leaf carried
     }
   }
 
 #pragma unroll
   for (int r = 0; r < MR; ++r) part[wave][r][lane] = y[r];
-  gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, 2>(g, part, last_flag, tid, grp, cg, m);
+  gv_finish<MR, PK_COLS, LEAVES, 64 * WAVES, LPW>(g, part, last_flag, tid, grp, cg, m);
 }
 
 // ---- 3 <= m <= 16 on the matrix cores, from the decode-packed layout.
@@ -470,9 +471,9 @@ static hipError_t launch_pk_mr(const GemvArgs& g, const float* x, int waves, dim
         break;
       }
       return hipErrorInvalidValue;
-    case PK_WAVES_SPLIT:  // few waves: every block of both leaves requested at once
-      hipLaunchKernelGGL((gemv_packed_kernel<MR, PK_WAVES_SPLIT, PK_BLOCKS>), grid, dim3(64 * PK_WAVES_SPLIT), 0, s,
-                         g, x);
+    case PK_WAVES_SPLIT:  // a small launch: 4-leaf groups as four one-leaf waves, every block in flight
+      hipLaunchKernelGGL((gemv_packed_kernel<MR, 2 * PK_WAVES_SPLIT, PK_BLOCKS, 1>), grid, dim3(128 * PK_WAVES_SPLIT),
+                         0, s, g, x);
       break;
     default:
       return hipErrorInvalidValue;
