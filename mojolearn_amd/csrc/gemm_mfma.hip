@@ -93,22 +93,6 @@ __device__ __forceinline__ void mfma_steps(v32f& acc, const char* la, const char
   }
 }
 
-// The tile of workgroup b among nb = tm x tn.  Workgroup b runs on XCD b % XCDS; the remap
-// gives XCD x a contiguous range of the tile sequence, in the order it dispatches them, and
-// the sequence walks bands of TILE_BAND row tiles column by column, so the 32 tiles an XCD runs
-// at once form a TILE_BAND x 8 block: the A row panels and B column panels they read are shared
-// in that XCD's L2 instead of fetched by every XCD.  A bijection of [0, nb): which tile a
-// workgroup computes never changes a cell's arithmetic.
-__device__ __forceinline__ int tile_of(int b, int nb, int tm, int tn) {
-  const int q = nb / XCDS, r = nb % XCDS;
-  const int x = b % XCDS, s = b / XCDS;
-  const int seq = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + s;
-  const int band = seq / (TILE_BAND * tn);
-  const int rows = tm - band * TILE_BAND < TILE_BAND ? tm - band * TILE_BAND : TILE_BAND;
-  const int local = seq - band * TILE_BAND * tn;
-  return (band * TILE_BAND + local % rows) * tn + local / rows;
-}
-
 // ACT: the store applies an activation follower (GemmArgs::epi 4 or 5; an instantiation of its
 // own, so the other products' kernels carry none of its code).
 template <int OP, int AT, int BT, bool ACT = false>

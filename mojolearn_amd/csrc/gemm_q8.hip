@@ -120,7 +120,7 @@ struct Q8Args {
   int64_t a_bytes, b_bytes;
   int32_t* part;        // split k: [splits][m][n] Int32 partial sums, else nullptr
   int64_t sps;          // 128-code slices per split (blockIdx.y)
-  int tiles_n;
+  int tiles_m, tiles_n;
 };
 
 constexpr int Q8_KS = KT * 4;  // codes per slice: 128
@@ -159,8 +159,10 @@ __global__ void __launch_bounds__(NTHREADS) q8_gemm_kernel(Q8Args g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 2;
   const int wc = wave & 3;
-  const int64_t i0 = (int64_t)(blockIdx.x / g.tiles_n) * BM;
-  const int64_t j0 = (int64_t)(blockIdx.x % g.tiles_n) * BN;
+  // the XCD-aware tile order (integer sums are exact: the order never changes a word)
+  const int tile = tile_of(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n);
+  const int64_t i0 = (int64_t)(tile / g.tiles_n) * BM;
+  const int64_t j0 = (int64_t)(tile % g.tiles_n) * BN;
   const int64_t nslices = (g.k + Q8_KS - 1) / Q8_KS;
   const int64_t kt0 = (int64_t)blockIdx.y * g.sps;
   const int64_t kt1 = kt0 + g.sps < nslices ? kt0 + g.sps : nslices;
@@ -425,7 +427,7 @@ struct Q15Args {
   int64_t a_bytes, b_bytes;
   int32_t* part;  // split k: [splits][3][m][n] Int32 partial sums (HH, MID, LL), else nullptr
   int64_t sps;    // slices per split
-  int tiles_n;
+  int tiles_m, tiles_n;
 };
 
 constexpr int Q15_SK = KT / 2;        // words per row per slice: 64 codes
@@ -465,8 +467,10 @@ __global__ void __launch_bounds__(NTHREADS) q15_gemm_kernel(Q15Args g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 2;
   const int wc = wave & 3;
-  const int64_t i0 = (int64_t)(blockIdx.x / g.tiles_n) * BM;
-  const int64_t j0 = (int64_t)(blockIdx.x % g.tiles_n) * BN;
+  // the XCD-aware tile order (integer sums are exact: the order never changes a word)
+  const int tile = tile_of(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n);
+  const int64_t i0 = (int64_t)(tile / g.tiles_n) * BM;
+  const int64_t j0 = (int64_t)(tile % g.tiles_n) * BN;
   const int64_t nslices = (g.k + Q15_KS - 1) / Q15_KS;
   const int64_t kt0 = (int64_t)blockIdx.y * g.sps;
   const int64_t kt1 = kt0 + g.sps < nslices ? kt0 + g.sps : nslices;
@@ -663,6 +667,7 @@ hipError_t run_q8_gemm(float* c, const int8_t* qa, const int32_t* ea, const int8
   g.a_bytes = m * pitch;
   g.b_bytes = n * pitch;
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  g.tiles_m = (int)tm;
   g.tiles_n = (int)tn;
   g.part = part;
   g.sps = sps;
@@ -840,6 +845,7 @@ hipError_t run_q15_gemm(float* c, const int8_t* ah, const int8_t* al, const int3
   g.part = part;
   g.sps = sps;
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  g.tiles_m = (int)tm;
   g.tiles_n = (int)tn;
   hipLaunchKernelGGL(q15_gemm_kernel, dim3((unsigned)(tm * tn), (unsigned)splits), dim3(NTHREADS), 0, stream, g);
   hipError_t e = hipGetLastError();
