@@ -11,8 +11,8 @@ mismatching words against the CPU oracle over every output cell (the output firs
 poison word), and the CPU baseline timed on the host cores: the scalar oracle on one thread on
 the reference's host-capped block (the headline `cpu_baseline`) and the reference's fast CPU
 column restated on every thread (with --all, both arms on every workload, and the host's CPU).
-Before the headline's W warmup steps the product runs untimed for CLOCK_RAMP_S seconds, which
-brings the engine clock to its steady state under this load; the K timed steps are unchanged.
+Just before the headline's timed run its captured graph replays untimed for CLOCK_RAMP_S seconds,
+which brings the engine clock to its steady state under this load; the K timed steps are unchanged.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
 """
@@ -34,11 +34,12 @@ HBM_PEAK_GBS = 8000.0
 EAGER = False  # --eager: time plain launches instead of graph replays (for counter runs)
 
 
-def graph_runs(calls, steps, warmup, torch, runs=1, eager=None):
+def graph_runs(calls, steps, warmup, torch, runs=1, eager=None, ramp_s=0.0, ramp_out=None):
     """Average ms per call of each of `runs` timed runs: `steps` calls (round-robin over `calls`,
     each a Plan) captured in one HIP graph on a private stream, replayed once per run; HIP events
     on the replaying stream.  With EAGER (or `eager`) the same calls are launched one by one on
-    that stream, bracketed by its events."""
+    that stream, bracketed by its events.  `ramp_s`: untimed replays of the graph for that many
+    seconds just before the timed runs (their count appended to `ramp_out`)."""
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         for i in range(max(warmup, len(calls))):
@@ -62,6 +63,13 @@ def graph_runs(calls, steps, warmup, torch, runs=1, eager=None):
             calls[i % len(calls)](s)
     g.replay()
     torch.cuda.synchronize()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < ramp_s:
+        g.replay()
+        torch.cuda.synchronize()
+        n += 1
+    if ramp_out is not None:
+        ramp_out.append(n * steps)
     cur = torch.cuda.current_stream()
     for _ in range(runs):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -78,30 +86,16 @@ def graph_time(calls, steps, warmup, torch):
     return graph_runs(calls, steps, warmup, torch)[0]
 
 
-#: seconds of untimed launches before the headline's warmup steps: the engine clock's ramp to its
-#: steady state under this load.  Measured with 20 timed steps after 5 warmup launches, the first
-#: timed run: 113.5 TFLOP/s with no ramp, 119-120 after 0.25 s, 123.5 after 1 s (the same kernel at
-#: a lower clock; 123-124 in steady state).
+#: seconds of untimed replays of the headline's graph just before its timed run: the engine
+#: clock's ramp to its steady state under this load (with 20 timed steps after 5 warmup launches
+#: and no ramp the first timed run read 113.5 TFLOP/s, against 123-124 in steady state: the same
+#: kernel at a lower clock).
 CLOCK_RAMP_S = 1.0
 
 
-def clock_ramp(calls, torch, seconds=CLOCK_RAMP_S):
-    """Untimed launches of `calls` on a private stream until `seconds` of wall time have passed;
-    the number of launches."""
-    s = torch.cuda.Stream()
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        with torch.cuda.stream(s):
-            for i in range(16):
-                calls[i % len(calls)](s)
-        s.synchronize()
-        n += 16
-    return n
-
-
-def _timed(calls, steps, warmup, torch, runs, eager=None):
+def _timed(calls, steps, warmup, torch, runs, eager=None, ramp_s=0.0, ramp_out=None):
     """{"ms": ...} from one run, or with runs > 1 the median run and the fastest and slowest."""
-    t = sorted(graph_runs(calls, steps, warmup, torch, runs, eager))
+    t = sorted(graph_runs(calls, steps, warmup, torch, runs, eager, ramp_s, ramp_out))
     if runs == 1:
         return {"ms": t[0]}
     return {"ms": float(np.median(t)), "ms_min": t[0], "ms_max": t[-1], "runs": runs}
@@ -143,14 +137,14 @@ def _t(torch, x):
 
 def bench_prefill(torch, D, W, O, steps, warmup, check, runs=1, cols=None, ramp=False):
     """The prefill projection; `cols` keeps W's and bias's first columns (one GPU's column
-    shard at its real shape); `ramp`: clock_ramp before the warmup steps."""
+    shard at its real shape); `ramp`: CLOCK_RAMP_S of untimed replays just before the timed run."""
     x, w, bias = W.prefill()
     if cols is not None:
         w, bias = np.ascontiguousarray(w[:, :cols]), np.ascontiguousarray(bias[:cols])
     plan = D.Plan(_t(torch, x), _t(torch, w), bias=_t(torch, bias))
-    ramped = clock_ramp([plan], torch) if ramp else 0
-    res = _timed([plan], steps, warmup, torch, runs)
-    res["ramp_launches"] = ramped
+    ramped = []
+    res = _timed([plan], steps, warmup, torch, runs, ramp_s=CLOCK_RAMP_S if ramp else 0.0, ramp_out=ramped)
+    res["ramp_launches"] = ramped[0] if ramped else 0
     res["out"] = None
     ms = res["ms"]
     m, k = x.shape
