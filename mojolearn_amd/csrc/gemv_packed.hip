@@ -18,8 +18,11 @@
 // are packed as zero codes and never stored.  The arithmetic and its order are gemv_nn_kernel's:
 // per leaf the chain acc = fma(x, f32(code) * scale, acc) in step order from +0, the level-1
 // pair of a wave's two leaves added in registers, the rest of the tree over the workgroup's
-// pairs (gv_finish with two-leaf nodes), and past 32 leaves the group roots folded by the workgroup that
-// completes the count -- so the bits are the row-major product's.
+// pairs (gv_finish with two-leaf nodes), and past 32 leaves the group roots folded by the
+// workgroup that completes the count -- so the bits are the row-major product's.  A launch too
+// small for whole columns runs 4-leaf groups of four one-leaf waves, folded across workgroups;
+// for 3 <= m <= 16 with x on the 16-byte grid the chains run on the matrix cores
+// (gemv_packed_mfma_kernel below).
 #include "gemv_body.h"
 
 namespace mlg {
