@@ -32,6 +32,7 @@ constexpr int GV_MAXM = 16;
 constexpr int GV_CH = 128;                  // W rows per register buffer: a whole contract leaf
 constexpr int GV_FOLD_BATCH = 16;           // root loads in flight while folding
 constexpr int GV_FEW_GROUPS = 8;            // up to this many groups: all roots loaded at once
+constexpr int GV_NT = 2;                    // buffer-load cache policy nt: streamed, not kept
 
 // Columns per lane: OP_NT one; OP_NN one 32-bit word, or (FULL: whole 128-row leaves) a
 // 16-bit word of int8 codes.

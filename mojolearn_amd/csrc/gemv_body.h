@@ -174,9 +174,12 @@ __device__ __forceinline__ void gv_leaf_full(float (&acc)[MR][CPL], const char* 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(wleaf) + (int64_t)b * GV_RB * rowbytes, (short)0,
                                              0x7FFFFFFF, RSRC_WORD3);
   };
+  // non-temporal (cache policy nt): a wave's loads of a row take whole lines, nothing is read
+  // twice (M=1 int8 decode 15.05 -> 14.5 us, fp32 GEMV 1x14336x4096 45.3 -> 43.2 us; the
+  // matrix-core kernels keep the default policy: M=16 31.7 -> 32.9 us with it)
   auto load_word = [&](__amdgpu_buffer_rsrc_t rs, int soff) -> uint32_t {
-    if constexpr (HALF) return __builtin_amdgcn_raw_buffer_load_b16(rs, (int)loff, soff, 0);
-    else return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, soff, 0);
+    if constexpr (HALF) return __builtin_amdgcn_raw_buffer_load_b16(rs, (int)loff, soff, GV_NT);
+    else return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)loff, soff, GV_NT);
   };
   const float* xr[MR];
 #pragma unroll
