@@ -204,15 +204,13 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
 // x[r][steps 4u .. 4u+3 of the block] of one leaf (one 16-byte read a leaf a block, block u
 // broadcast for steps 4u .. 4u+3); with SHAPE 4, lane 32g + 16q + 4u + r holds x[4g + r][steps
 // 4u .. 4u+3] of leaf q (one read a block for both leaves and both groups, block 8g + 4q + u
-// broadcast).  x travels through LDS: each wave streams its leaves' x for the next blocks into a
-// ring of its own LDS slots with direct-to-LDS loads, issued with the block's weights, lane L's
-// chunk at L * 16.  The workgroup and its fold are gemv_packed_kernel's.
+// broadcast).  So each lane loads its own x chunks straight into registers, with the block's
+// weights.  The workgroup and its fold are gemv_packed_kernel's.
 template <int SHAPE, int G>
 struct PkMf {
   static constexpr int MR = SHAPE == 16 ? 16 : 4 * G;  // rows the lane's instructions cover
   static constexpr int NA = SHAPE == 16 ? 1 : G;        // accumulators a leaf
-  static constexpr int NI = SHAPE == 16 ? 2 : 1;        // x loads (and reads) a block, 1 KB each
-  static constexpr int SLOT = NI * 1024;                // bytes of one ring slot
+  static constexpr int NI = SHAPE == 16 ? 2 : 1;        // x loads a block, 16 bytes a lane each
 };
 typedef float pk_v16f __attribute__((ext_vector_type(16)));
 typedef float pk_v4f __attribute__((ext_vector_type(4)));
@@ -220,8 +218,8 @@ template <int SHAPE>
 using PkV = typename std::conditional<SHAPE == 16, pk_v16f, pk_v4f>::type;
 
 // The x chunk lane l of load h holds: leaf q, row r, steps 4u .. 4u+3 of the block (the
-// broadcast layout above; with one group of four rows, lanes 32 .. 63 load nothing and their
-// half of the slot is never read).
+// broadcast layout above; with one group of four rows, lanes 32 .. 63 load nothing: no
+// instruction takes their x).
 template <int SHAPE, int G>
 __device__ __forceinline__ void pk_xchunk(int h, int lane, int& q, int& r, int& u) {
   if constexpr (SHAPE == 16) {
@@ -237,7 +235,7 @@ __device__ __forceinline__ void pk_xchunk(int h, int lane, int& q, int& r, int& 
 }
 
 // f(integral_constant<int, I>) for I = B .. E-1: the block loop with its index a constant, so
-// every wait count and LDS slot below is named at compile time.
+// every wait count and register slot below is named at compile time.
 template <int B, int E, typename F>
 __device__ __forceinline__ void pk_static_for(F&& f) {
   if constexpr (B < E) {
@@ -253,73 +251,50 @@ __device__ __forceinline__ void pk_wait_vm() {
   __builtin_amdgcn_s_waitcnt(((N & 15) | ((N >> 4) << 14)) | 0x0F70);
 }
 
-// The NSLOT x slots of one wave, each in its own __shared__ array: the compiler tracks the
-// direct-to-LDS loads per array, so a read of one slot waits only for that slot's loads.
-template <int NSLOT>
-struct PkSlots {
-  char* p[NSLOT];
-};
-
 // NL adjacent leaves of one lane's column (block s of leaf q at base + s * slab + q * lstride,
 // + lane * 16), AHEAD blocks in flight.  Issue order: blocks 0 .. AHEAD-1 (weights, then x) up
-// front; in iteration s the weights of block s + AHEAD before block s is consumed and its x into
-// the slot block s has just freed after.  x slots: AHEAD of them, block s in slot s % AHEAD.
+// front; in iteration s block s + AHEAD's weights and x before block s is consumed.  Both land
+// in register rings of AHEAD + 1 blocks; a lane's x chunk is the one its own instructions take.
 template <int SHAPE, int G, int NL, int AHEAD, typename V, int NA>
 __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* base, int64_t slab, int lstride,
                                                int lane, __amdgpu_buffer_rsrc_t xrs,
-                                               const uint32_t (&xvoff)[PkMf<SHAPE, G>::NI],
-                                               const PkSlots<AHEAD>& slots, float sc) {
+                                               const uint32_t (&xvoff)[PkMf<SHAPE, G>::NI], float sc) {
   using S = PkMf<SHAPE, G>;
   static_assert(NA == S::NA, "accumulators a leaf");
   static_assert(AHEAD >= 1 && AHEAD <= PK_BLOCKS, "blocks in flight");
-  constexpr int MR = S::MR;
-  constexpr int RING = AHEAD + 1 < PK_BLOCKS ? AHEAD + 1 : PK_BLOCKS;  // weight registers
+  constexpr int RING = AHEAD + 1 < PK_BLOCKS ? AHEAD + 1 : PK_BLOCKS;  // register blocks
   constexpr int LPG = S::NI + NL;                                    // loads a block
   auto block_rs = [&](int s) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + s * slab, (short)0, 0x7FFFFFFF, RSRC_WORD3);
   };
   u4 ring[RING][NL];
-  auto issue_w = [&](int s) {
+  u4 xr[RING][S::NI];
+  // (with one group of four rows only lanes 0 .. 31 load x: the other half would repeat them)
+  auto issue = [&](int s) {
 #pragma unroll
     for (int q = 0; q < NL; ++q)
       ring[s % RING][q] = __builtin_amdgcn_raw_buffer_load_b128(block_rs(s), lane * 16, q * lstride, PK_AUX);
-  };
-  // (with one group of four rows only lanes 0 .. 31 load: the other half of the chunk would repeat them)
-  auto issue_x = [&](auto SC) {
-    constexpr int s = decltype(SC)::value;
 #pragma unroll
-    for (int h = 0; h < S::NI; ++h) {
-      if (SHAPE == 16 || G == 2 || lane < 32) {
-#if defined(__HIP_DEVICE_COMPILE__)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_vptr)(slots.p[s % AHEAD] + h * 1024), 16, xvoff[h], 64 * s,
-                                                 0, 0);
-#endif
-      }
-    }
+    for (int h = 0; h < S::NI; ++h)
+      if (SHAPE == 16 || G == 2 || lane < 32)
+        xr[s % RING][h] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)xvoff[h], 64 * s, 0);
   };
-  pk_static_for<0, AHEAD>([&](auto SC) {
-    issue_w(decltype(SC)::value);
-    issue_x(SC);
-  });
+  pk_static_for<0, AHEAD>([&](auto SC) { issue(decltype(SC)::value); });
 
   pk_static_for<0, PK_BLOCKS>([&](auto SC) {
     constexpr int s = decltype(SC)::value;
     if constexpr (s + AHEAD < PK_BLOCKS) {
       __builtin_amdgcn_sched_barrier(0);
-      issue_w(s + AHEAD);
+      issue(s + AHEAD);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // block s landed, its x included; the loads issued after its x stay in flight
-    constexpr int full = PK_BLOCKS - 1 - s < AHEAD - 1 ? PK_BLOCKS - 1 - s : AHEAD - 1;
-    constexpr int after = full * LPG + (s + AHEAD < PK_BLOCKS ? NL : 0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    pk_wait_vm<after>();
+    // block s landed; the blocks issued after it stay in flight
+    constexpr int later = PK_BLOCKS - 1 - s < AHEAD ? PK_BLOCKS - 1 - s : AHEAD;
+    pk_wait_vm<later * LPG>();
     __builtin_amdgcn_sched_barrier(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    const char* slot = slots.p[s % AHEAD];
     f4 xq[S::NI];
 #pragma unroll
-    for (int h = 0; h < S::NI; ++h) xq[h] = *reinterpret_cast<const f4*>(slot + h * 1024 + lane * 16);
+    for (int h = 0; h < S::NI; ++h) xq[h] = __builtin_bit_cast(f4, xr[s % RING][h]);
     pk_static_for<0, PK_RB>([&](auto BC) {
       constexpr int b = decltype(BC)::value;  // byte of the chunk: row 16 s + b of the leaf
       pk_static_for<0, NL>([&](auto QC) {
@@ -337,12 +312,6 @@ __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* bas
         });
       });
     });
-    if constexpr (s + AHEAD < PK_BLOCKS) {
-      // the slot's reads above have returned (their values fed the instructions)
-      __builtin_amdgcn_sched_barrier(0);
-      issue_x(std::integral_constant<int, s + AHEAD>{});
-      __builtin_amdgcn_sched_barrier(0);
-    }
   });
 }
 
@@ -352,16 +321,6 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_mfma_kernel(GemvArgs g
   using V = PkV<SHAPE>;
   constexpr int MR = S::MR;
   constexpr int LEAVES = 2 * WAVES;
-  // x slots: one __shared__ array each (unused ones 16 bytes)
-  constexpr int SL = WAVES * S::SLOT;
-  __shared__ __attribute__((aligned(1024))) char xs0[AHEAD > 0 ? SL : 16];
-  __shared__ __attribute__((aligned(1024))) char xs1[AHEAD > 1 ? SL : 16];
-  __shared__ __attribute__((aligned(1024))) char xs2[AHEAD > 2 ? SL : 16];
-  __shared__ __attribute__((aligned(1024))) char xs3[AHEAD > 3 ? SL : 16];
-  __shared__ __attribute__((aligned(1024))) char xs4[AHEAD > 4 ? SL : 16];
-  __shared__ __attribute__((aligned(1024))) char xs5[AHEAD > 5 ? SL : 16];
-  __shared__ __attribute__((aligned(1024))) char xs6[AHEAD > 6 ? SL : 16];
-  __shared__ __attribute__((aligned(1024))) char xs7[AHEAD > 7 ? SL : 16];
   __shared__ __attribute__((aligned(16))) float part[WAVES][MR][PK_COLS];
   __shared__ unsigned int last_flag;
 
@@ -400,18 +359,14 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_mfma_kernel(GemvArgs g
       const int64_t row = r < m ? r : m - 1;
       xvoff[h] = (uint32_t)((row * g.k + (t0 + q) * GV_CH + 4 * u) * 4);
     }
-    PkSlots<AHEAD> slots;
-    char* all[8] = {xs0, xs1, xs2, xs3, xs4, xs5, xs6, xs7};
-#pragma unroll
-    for (int i = 0; i < AHEAD; ++i) slots.p[i] = all[i] + wave * S::SLOT;
     if (t0 + 1 < g.nleaves) {
       V acc[2][S::NA];
-      pk_leaves_mfma<SHAPE, G, 2, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, slots, sc);
+      pk_leaves_mfma<SHAPE, G, 2, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
 #pragma unroll
       for (int gg = 0; gg < S::NA; ++gg) y[gg] = acc[0][gg] + acc[1][gg];  // the level-1 pair
     } else {
       V acc[1][S::NA];
-      pk_leaves_mfma<SHAPE, G, 1, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, slots, sc);
+      pk_leaves_mfma<SHAPE, G, 1, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
 #pragma unroll
       for (int gg = 0; gg < S::NA; ++gg) y[gg] = acc[0][gg];  // the odd last leaf, carried
     }
