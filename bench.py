@@ -13,8 +13,9 @@ the reference's host-capped block (the headline `cpu_baseline`) and the referenc
 column restated on every thread (with --all, both arms on every workload, and the host's CPU).
 Just before the headline's timed run its captured graph replays untimed for CLOCK_RAMP_S seconds,
 which brings the engine clock to its steady state under this load; the K timed steps are unchanged.
+The decode rows and read floors do the same (--decode-ramp seconds; 0 for kernel-trace runs).
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu] [--decode-ramp S]
 """
 import argparse
 import json
@@ -91,6 +92,10 @@ def graph_time(calls, steps, warmup, torch):
 #: and no ramp the first timed run read 113.5 TFLOP/s, against 123-124 in steady state: the same
 #: kernel at a lower clock).
 CLOCK_RAMP_S = 1.0
+#: the same untimed ramp before each decode row and read floor (set by --decode-ramp): with 100
+#: warmup launches of a 12-17 us kernel (1.5 ms) the clock has not settled either (M=4 16.5 us,
+#: against 15.6 after 0.75 s of launches).
+DECODE_RAMP_S = CLOCK_RAMP_S
 
 
 def _timed(calls, steps, warmup, torch, runs, eager=None, ramp_s=0.0, ramp_out=None):
@@ -200,7 +205,9 @@ def bench_decode(torch, D, W, O, m, steps, warmup, check, nbuf=8, runs=1, cols=N
         plans = [D.PackedPlan(tx, p, ts, out=out) for p in pw]
     else:
         plans = [D.Plan(tx, tc, scales=ts, out=out) for tc in tcodes]
-    res = _timed(plans, max(steps, 2 * nbuf), warmup, torch, runs)
+    ramped = []
+    res = _timed(plans, max(steps, 2 * nbuf), warmup, torch, runs, ramp_s=DECODE_RAMP_S, ramp_out=ramped)
+    res["ramp_launches"] = ramped[0] if ramped else 0
     ms = res["ms"]
     k, n = codes.shape
     nbytes = k * n + 4 * n + 4 * m * k + 4 * m * n
@@ -236,7 +243,9 @@ def bench_read_floor(torch, steps, warmup, runs, nbuf=8):
     for pattern, name in ((0, "linear"), (1, "leaf"), (2, "packed")):
         calls = [lambda s, b=b, pattern=pattern: _native.check(
             L.mlg_stream_read(b.data_ptr(), k, n, pattern, sink.data_ptr(), s.cuda_stream)) for b in bufs]
-        r = _timed(calls, max(steps, 2 * nbuf), warmup, torch, runs)
+        ramped = []
+        r = _timed(calls, max(steps, 2 * nbuf), warmup, torch, runs, ramp_s=DECODE_RAMP_S, ramp_out=ramped)
+        r["ramp_launches"] = ramped[0] if ramped else 0
         r.update({"us": r["ms"] * 1e3, "gbs": k * n / (r["ms"] * 1e-3) / 1e9,
                   "hbm_frac": k * n / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes": k * n})
         res[name] = r
@@ -651,6 +660,9 @@ def main():
                     help="also measure the rows the reference publishes for this path (MI325X)")
     ap.add_argument("--read-floor", action="store_true",
                     help="only time the read-only streams over the decode weight buffers and exit")
+    ap.add_argument("--decode-ramp", type=float, default=CLOCK_RAMP_S,
+                    help="seconds of untimed graph replays before each decode row and read floor "
+                         "(0 for kernel-trace runs: every replay is traced)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (the byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -668,8 +680,9 @@ def main():
     if args.read_floor:
         print(json.dumps({"read_floor": bench_read_floor(torch, args.steps, args.warmup, runs=20)}), flush=True)
         return
-    global EAGER
+    global EAGER, DECODE_RAMP_S
     EAGER = args.eager
+    DECODE_RAMP_S = args.decode_ramp
 
     from mojolearn_amd import device as D
     from mojolearn_amd import workloads as W
