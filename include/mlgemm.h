@@ -125,7 +125,8 @@ int mlg_gemm_noalloc(float* c, const void* a, const void* b, const float* scales
  * op NN), for callers that keep a weight resident across many decode steps and can rearrange
  * it once.  codes[k][n] (k a positive multiple of 128 with at most 1024 leaves of 128, n >= 1)
  * becomes a copy of mlg_int8w_packed_bytes(k, n) = k * 64 * ceil(n / 64) bytes in which code
- * (p, j) sits at ((s * P + t) * G + g) * 1024 + l * 16 + i, with P = k / 128 leaves,
+ * (p, j), biased to the unsigned byte code + 128, sits at ((s * P + t) * G + g) * 1024 + l * 16 + i,
+ * with P = k / 128 leaves,
  * t = p / 128, s = (p % 128) / 16, i = p % 16, G = ceil(n / 64) groups, g = j / 64, l = j % 64
  * (columns past n are zero codes): sixteen rows of one column are one 16-byte word, a 64-column
  * group's block is one 1 KB chunk, and block s of every leaf is one contiguous slab.

@@ -6,7 +6,7 @@
 // leaf groups of a column meet through a cross-workgroup fold (roots to memory, a counter, the
 // last workgroup reloading them).  The packed layout makes a 64-column group contiguous:
 // code (p, j) -- leaf t = p / 128, block s = (p % 128) / 16 (sixteen rows), row i = p % 16,
-// column group cg = j / 64, lane l = j % 64 -- lives at byte
+// column group cg = j / 64, lane l = j % 64 -- lives, biased (the byte code + 128), at byte
 //
 //     ((s * P + t) * ncg + cg) * 1024 + l * 16 + i        (P leaves, ncg column groups),
 //
@@ -15,7 +15,9 @@
 // which advance together, read at the same time.  A workgroup of 16 waves, each running two
 // adjacent leaves, then holds 32 leaves of 64 columns: at K = 4096 the whole contract tree of
 // its columns, folded in LDS with no workspace, no counter and no second pass.  Columns past n
-// are packed as zero codes and never stored.  The arithmetic and its order are gemv_nn_kernel's:
+// are packed as zero codes and never stored.  The bias lets the dequant convert an unsigned byte
+// (v_cvt_f32_ubyte, faster than the sign-extending convert) and fold the bias into one fma
+// (pk_dequant).  The arithmetic and its order are gemv_nn_kernel's:
 // per leaf the chain acc = fma(x, f32(code) * scale, acc) in step order from +0, the level-1
 // pair of a wave's two leaves added in registers, the rest of the tree over the workgroup's
 // pairs (gv_finish with two-leaf nodes), and past 32 leaves the group roots folded by the
@@ -36,6 +38,24 @@ constexpr int PK_CHUNK_THREADS = 256;
 constexpr int PK_AHEAD = 2;
 // The weight loads are non-temporal (cache policy nt: streamed, not kept in L2): 12.4 -> 11.5 us.
 constexpr int PK_AUX = 2;
+constexpr uint32_t PK_BIAS = 0x80808080u;  // code + 128 in each byte of a packed word
+
+// f32(code) * scale with one rounding (the contract's dequant; the scale is flushed on input by
+// MODE.FP_DENORM = 2) from byte `byte` of a packed word.  FAST: f32(u) * scale - 128 * scale is
+// code * scale exactly, so one fma rounds it once, whenever 128 * scale is exact (nsc = -128 *
+// scale, |scale| < 2^120 and not NaN: the caller's wave-uniform check).  Otherwise the code is
+// unbiased, sign-extended and multiplied.  A zero weight's sign cannot reach a chain that
+// starts at +0 (+0 + -0 is +0), so the forms agree on every bit that reaches the output.
+template <bool FAST>
+__device__ __forceinline__ float pk_dequant(uint32_t u, int byte, float sc, float nsc) {
+  if constexpr (FAST) return __builtin_fmaf((float)((u >> (8 * byte)) & 0xFFu), sc, nsc);
+  else return (float)((int32_t)((u ^ PK_BIAS) << (24 - 8 * byte)) >> 24) * sc;
+}
+
+// Whether every lane of the wave may take pk_dequant's fma form.
+__device__ __forceinline__ bool pk_fast_scales(float sc) {
+  return __builtin_amdgcn_ballot_w64(!(__builtin_fabsf(sc) < 0x1p120f)) == 0;
+}
 
 // One thread per 16-byte chunk (block s, leaf t, group cg, lane l), chunk index
 // ((s * P + t) * ncg + cg) * 64 + l: it gathers rows 16s .. 16s+15 of leaf t at column
@@ -58,17 +78,18 @@ __global__ void __launch_bounds__(PK_CHUNK_THREADS) int8w_pack_kernel(u4* __rest
 #pragma unroll
     for (int i = 0; i < PK_RB; ++i) w[i >> 2] |= (uint32_t)codes[(p0 + i) * n + j] << (8 * (i & 3));
   }
-  dst[chunk] = u4{w[0], w[1], w[2], w[3]};
+  dst[chunk] = u4{w[0] ^ PK_BIAS, w[1] ^ PK_BIAS, w[2] ^ PK_BIAS, w[3] ^ PK_BIAS};
 }
 
 // NL adjacent leaves of one lane's column from the packed layout: block s of leaf q at
 // base + s * slab + q * lstride (+ lane * 16), AHEAD blocks requested ahead of the one
 // consumed.  x is read XB steps at a time (uniform loads) one batch ahead.  acc[q][r] is leaf
 // q's chain for row r.
-template <int MR, int NL, int AHEAD>
+template <int MR, int NL, int AHEAD, bool FAST>
 __device__ __forceinline__ void gv_leaves_packed(float (&acc)[NL][MR], const char* base, int64_t slab,
                                                  int lstride, int lane, const float* __restrict__ xl, int64_t k,
                                                  int m, float sc) {
+  const float nsc = -128.f * sc;  // exact for pk_dequant<true>
   constexpr int XB = MR * NL <= 2 ? 8 : (16 / (MR * NL) < 2 ? 2 : 16 / (MR * NL));  // steps a batch
   auto block_rs = [&](int s) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + s * slab, (short)0, 0x7FFFFFFF, RSRC_WORD3);
@@ -116,8 +137,7 @@ __device__ __forceinline__ void gv_leaves_packed(float (&acc)[NL][MR], const cha
 #pragma unroll
         for (int q = 0; q < NL; ++q) {
           const uint32_t u = ring[s][q][b >> 2];
-          // f32(code) * scale, one rounding (the scale flushed on input by MODE.FP_DENORM = 2)
-          const float w = (float)((int32_t)(u << (24 - 8 * (b & 3))) >> 24) * sc;
+          const float w = pk_dequant<FAST>(u, b & 3, sc, nsc);
 #pragma unroll
           for (int r = 0; r < MR; ++r) acc[q][r] = __builtin_fmaf(xc[r][q][i], w, acc[q][r]);
         }
@@ -170,14 +190,20 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_kernel(GemvArgs g, con
       float acc[2][MR];
 #pragma unroll
       for (int r = 0; r < MR; ++r) acc[0][r] = acc[1][r] = 0.f;
-      gv_leaves_packed<MR, 2, AHEAD>(acc, base, slab, lstride, lane, x + t0 * GV_CH, g.k, m, sc);
+      if (pk_fast_scales(sc))
+        gv_leaves_packed<MR, 2, AHEAD, true>(acc, base, slab, lstride, lane, x + t0 * GV_CH, g.k, m, sc);
+      else
+        gv_leaves_packed<MR, 2, AHEAD, false>(acc, base, slab, lstride, lane, x + t0 * GV_CH, g.k, m, sc);
 #pragma unroll
       for (int r = 0; r < MR; ++r) y[r] = acc[0][r] + acc[1][r];  // the level-1 pair
     } else {
       float acc[1][MR];
 #pragma unroll
       for (int r = 0; r < MR; ++r) acc[0][r] = 0.f;
-      gv_leaves_packed<MR, 1, AHEAD>(acc, base, slab, lstride, lane, x + t0 * GV_CH, g.k, m, sc);
+      if (pk_fast_scales(sc))
+        gv_leaves_packed<MR, 1, AHEAD, true>(acc, base, slab, lstride, lane, x + t0 * GV_CH, g.k, m, sc);
+      else
+        gv_leaves_packed<MR, 1, AHEAD, false>(acc, base, slab, lstride, lane, x + t0 * GV_CH, g.k, m, sc);
 #pragma unroll
       for (int r = 0; r < MR; ++r) y[r] = acc[0][r];  // one leaf, or the odd last leaf carried
     }
@@ -255,10 +281,11 @@ __device__ __forceinline__ void pk_wait_vm() {
 // + lane * 16), AHEAD blocks in flight.  Issue order: blocks 0 .. AHEAD-1 (weights, then x) up
 // front; in iteration s block s + AHEAD's weights and x before block s is consumed.  Both land
 // in register rings of AHEAD + 1 blocks; a lane's x chunk is the one its own instructions take.
-template <int SHAPE, int G, int NL, int AHEAD, typename V, int NA>
+template <int SHAPE, int G, int NL, int AHEAD, bool FAST, typename V, int NA>
 __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* base, int64_t slab, int lstride,
                                                int lane, __amdgpu_buffer_rsrc_t xrs,
                                                const uint32_t (&xvoff)[PkMf<SHAPE, G>::NI], float sc) {
+  const float nsc = -128.f * sc;  // exact for pk_dequant<true>
   using S = PkMf<SHAPE, G>;
   static_assert(NA == S::NA, "accumulators a leaf");
   static_assert(AHEAD >= 1 && AHEAD <= PK_BLOCKS, "blocks in flight");
@@ -300,8 +327,7 @@ __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* bas
       pk_static_for<0, NL>([&](auto QC) {
         constexpr int q = decltype(QC)::value;
         const uint32_t u = ring[s % RING][q][b >> 2];
-        // f32(code) * scale, one rounding (the scale flushed on input by MODE.FP_DENORM = 2)
-        const float w = (float)((int32_t)(u << (24 - 8 * (b & 3))) >> 24) * sc;
+        const float w = pk_dequant<FAST>(u, b & 3, sc, nsc);
         pk_static_for<0, NA>([&](auto GC) {
           constexpr int gg = decltype(GC)::value;
           const V c = (s == 0 && b == 0) ? V{} : acc[q][gg];
@@ -361,12 +387,18 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_packed_mfma_kernel(GemvArgs g
     }
     if (t0 + 1 < g.nleaves) {
       V acc[2][S::NA];
-      pk_leaves_mfma<SHAPE, G, 2, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
+      if (pk_fast_scales(sc))
+        pk_leaves_mfma<SHAPE, G, 2, AHEAD, true>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
+      else
+        pk_leaves_mfma<SHAPE, G, 2, AHEAD, false>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
 #pragma unroll
       for (int gg = 0; gg < S::NA; ++gg) y[gg] = acc[0][gg] + acc[1][gg];  // the level-1 pair
     } else {
       V acc[1][S::NA];
-      pk_leaves_mfma<SHAPE, G, 1, AHEAD>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
+      if (pk_fast_scales(sc))
+        pk_leaves_mfma<SHAPE, G, 1, AHEAD, true>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
+      else
+        pk_leaves_mfma<SHAPE, G, 1, AHEAD, false>(acc, base, slab, lstride, lane, xrs, xvoff, sc);
 #pragma unroll
       for (int gg = 0; gg < S::NA; ++gg) y[gg] = acc[0][gg];  // the odd last leaf, carried
     }

@@ -31,13 +31,14 @@ def _bits(x):
 
 
 def packed_layout(codes):
-    """The decode-packed bytes of codes[k][n] (k a multiple of 128)."""
+    """The decode-packed bytes of codes[k][n] (k a multiple of 128): each code biased to the
+    unsigned byte code + 128 (columns past n hold code 0, byte 128)."""
     k, n = codes.shape
     P, G = k // 128, -(-n // 64)
     pad = np.zeros((k, G * 64), np.int8)
     pad[:, :n] = codes
     a = pad.reshape(P, 8, 16, G, 64).transpose(1, 0, 3, 4, 2)
-    return np.ascontiguousarray(a).reshape(-1).view(np.uint8)
+    return np.ascontiguousarray(a).reshape(-1).view(np.uint8) ^ np.uint8(0x80)
 
 
 @pytest.mark.parametrize("k,n", [(128, 1), (256, 130), (1152, 257), (4096, 300), (4480, 8196)])
@@ -82,8 +83,10 @@ def test_packed_gemv_parity(oracle, shape):
     x = _x(rng, m, k, special)
     codes = rng.integers(-127, 128, (k, n), dtype=np.int8)
     scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
-    if special:  # extreme scales: subnormal (flushed on input), zero, huge, tiny normal
-        scales[: min(n, 4)] = np.array([1e-40, 0.0, 3e37, 1.2e-38], np.float32)[: min(n, 4)]
+    if special:  # extreme scales: subnormal (flushed on input), zero, huge (past the exact fma
+        # form's 2^120: its wave takes the sign-extended dequant), tiny normal, infinite, NaN
+        sv = np.array([1e-40, 0.0, 3e37, 1.2e-38, np.inf, -np.inf, np.nan], np.float32)
+        scales[: min(n, sv.size)] = sv[: min(n, sv.size)]
     bias = rng.standard_normal(n).astype(np.float32) if k % 256 == 0 else None
     print(f"packed gemv m={m} n={n} k={k} special={special} bias={bias is not None}", flush=True)
     tx, tc, ts = _t(x), _t(codes), _t(scales)
