@@ -112,6 +112,9 @@ __device__ __forceinline__ void gv_leaves_packed(float (&acc)[NL][MR], const cha
       for (int i = 0; i < XB; ++i) xc[r][q][i] = xr[r][q * GV_CH + i];
 #pragma unroll
   for (int s = 0; s < PK_BLOCKS; ++s) {
+    // a block issues no loads once every block is in flight: the fence keeps its converts from
+    // being hoisted into earlier blocks (all of them live at once: 55 -> 137 VGPRs at M = 1)
+    if (s + AHEAD >= PK_BLOCKS) __builtin_amdgcn_sched_barrier(0);
     if (s + AHEAD < PK_BLOCKS) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
