@@ -107,6 +107,36 @@ def test_packed_gemv_parity(oracle, shape):
     assert np.array_equal(_bits(rowmajor), _bits(got))
 
 
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_packed_gemv_dequant_forms_at_their_boundary(oracle, m):
+    """The dequant's fma form (f32(code + 128) * scale - 128 * scale) holds for |scale| < 2^120;
+    a wave with any larger scale takes the sign-extended form.  Scales just below and at 2^120
+    (products up to 127 * 2^120, finite), the largest and smallest normal floats and ordinary
+    ones, in different waves and in one wave together: the bits of the oracle's rn(f32(code) *
+    scale) chains either way."""
+    from mojolearn_amd import device as D
+    k, n = 4096, 12288  # whole-column workgroups (192 groups fill the CUs)
+    rng = np.random.default_rng(m + 120)
+    x = (rng.standard_normal((m, k)) * 2.0 ** -100).astype(np.float32)  # keeps sums finite
+    codes = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    edge = np.array([np.nextafter(np.float32(2.0 ** 120), np.float32(0)), np.float32(2.0 ** 120),
+                     np.float32(3.4e38), np.float32(1.17549435e-38), np.float32(-2.0 ** 119)], np.float32)
+    scales = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    scales[:64] = edge[np.arange(64) % edge.size]      # one group: every wave of it falls back
+    scales[64:128] = edge[0]                           # just below: the fma form
+    scales[128:192] = -edge[0]
+    scales[200] = edge[1]                              # one lane at 2^120 in an ordinary group
+    print(f"packed gemv dequant boundary: m={m} n={n} k={k}", flush=True)
+    packed = D.pack_int8w(_t(codes))
+    want = oracle.nan_canon(oracle.gemm_fast(x, oracle.int8_dequant(codes, scales, 0), 0))
+    out = torch.full((m, n), POISON, dtype=torch.float32, device=DEV)
+    D.gemv_int8w_packed(_t(x), packed, _t(scales), out=out)
+    torch.cuda.synchronize()
+    got = oracle.nan_canon(out.cpu().numpy())
+    bad = np.flatnonzero(_bits(got) != _bits(want))
+    assert bad.size == 0, f"{bad.size} words differ, first at {divmod(int(bad[0]), n)}"
+
+
 @pytest.mark.parametrize("m,n,k", [(3, 14336, 4096), (8, 300, 1024), (16, 12288, 4096)])
 def test_packed_gemv_x_off_the_16_byte_grid(oracle, m, n, k):
     """x at a 4-byte offset: the matrix-core kernel loads x in 16-byte chunks, so these products
