@@ -325,12 +325,23 @@ __device__ __forceinline__ void pk_leaves_mfma(V (&acc)[NL][NA], const char* bas
     f4 xq[S::NI];
 #pragma unroll
     for (int h = 0; h < S::NI; ++h) xq[h] = __builtin_bit_cast(f4, xr[s % RING][h]);
+    // the block's weights first, then its instructions back to back: with each weight formed just
+    // before its instruction, every instruction waited on its own convert and fma (and the SIMD's
+    // waves, running the same sequence, on theirs): M = 4 14.7 -> 13.2 us, M = 16 25.3 -> 23.7
+    float wb[PK_RB][NL];
+    pk_static_for<0, PK_RB>([&](auto BC) {
+      constexpr int b = decltype(BC)::value;
+      pk_static_for<0, NL>([&](auto QC) {
+        constexpr int q = decltype(QC)::value;
+        wb[b][q] = pk_dequant<FAST>(ring[s % RING][q][b >> 2], b & 3, sc, nsc);
+      });
+    });
+    __builtin_amdgcn_sched_barrier(0);
     pk_static_for<0, PK_RB>([&](auto BC) {
       constexpr int b = decltype(BC)::value;  // byte of the chunk: row 16 s + b of the leaf
       pk_static_for<0, NL>([&](auto QC) {
         constexpr int q = decltype(QC)::value;
-        const uint32_t u = ring[s % RING][q][b >> 2];
-        const float w = pk_dequant<FAST>(u, b & 3, sc, nsc);
+        const float w = wb[b][q];
         pk_static_for<0, NA>([&](auto GC) {
           constexpr int gg = decltype(GC)::value;
           const V c = (s == 0 && b == 0) ? V{} : acc[q][gg];
